@@ -1,0 +1,528 @@
+// Engine context and C ABI (include/furnace_hip.h).
+//
+// A context owns, on one gfx950 device: the raw GGUF weight blocks (one
+// allocation per tensor, uploaded once), the f32 KV cache, activation
+// buffers, the host-computed RoPE table and a StepState.  finalize() records
+// the decode step -- embedding, 28x (norm+QKV, RoPE+KV write, attention,
+// o-proj+residual, norm+gate/up+SwiGLU, down+residual), final norm + lm_head
+// + argmax -- into a hipGraph that is replayed once per token.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/furnace_hip.h"
+#include "common.hpp"
+#include "formats.hpp"
+#include "kernels.hpp"
+
+using namespace frn;
+
+#define fail frn_fail
+
+static frn_status hip_fail(hipError_t e, const char* what) {
+  return fail(e == hipErrorOutOfMemory ? FRN_EOOM : FRN_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+#define HIP_TRY(expr, what)                  \
+  do {                                       \
+    hipError_t e_ = (expr);                  \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+
+namespace {
+
+struct DevTensor {
+  uint32_t type = 0;
+  uint64_t out = 0, in = 0;
+  size_t bytes = 0;
+  uint8_t* ptr = nullptr;  // raw blocks, or f32 for 1-D tensors
+};
+
+struct LayerPtrs {
+  const float *attn_norm, *bq, *bk, *bv, *ffn_norm;
+  const DevTensor *wq, *wk, *wv, *wo, *gate, *up, *down;
+};
+
+size_t type_row_bytes(uint32_t t, uint64_t in) { return (size_t)(in / blk_elems(t)) * blk_bytes(t); }
+bool known_type(uint32_t t) { return t == T_F32 || t == T_Q5_0 || t == T_Q8_0 || t == T_Q4_K || t == T_Q6_K; }
+
+}  // namespace
+
+struct frn_ctx {
+  frn_config cfg{};
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::map<std::string, DevTensor> tensors;
+  std::vector<LayerPtrs> layers;
+  const DevTensor *embd = nullptr, *lm_head = nullptr;
+  const float* out_norm = nullptr;
+  float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *act = nullptr, *logits = nullptr;
+  float *part = nullptr, *kcache = nullptr, *vcache = nullptr, *rope = nullptr;
+  StepState* st = nullptr;
+  StepState* h_st = nullptr;  // pinned mirror for read-back
+  uint32_t len = 0;           // host view of KvCache::len
+  uint32_t last_next = 0xFFFFFFFFu;
+  bool finalized = false, have_logits = false;
+  hipGraphExec_t g_step = nullptr, g_prefill = nullptr;
+  hipGraph_t graph_step = nullptr, graph_prefill = nullptr;
+  bool timing = false;
+  double t_ms[9] = {0};
+  uint64_t t_calls[9] = {0};
+};
+
+static void free_ctx(frn_ctx* c) {
+  if (!c) return;
+  if (c->g_step) (void)hipGraphExecDestroy(c->g_step);
+  if (c->g_prefill) (void)hipGraphExecDestroy(c->g_prefill);
+  if (c->graph_step) (void)hipGraphDestroy(c->graph_step);
+  if (c->graph_prefill) (void)hipGraphDestroy(c->graph_prefill);
+  for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->att, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st};
+  for (void* p : bufs)
+    if (p) (void)hipFree(p);
+  if (c->h_st) (void)hipHostFree(c->h_st);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+template <typename T>
+static hipError_t dmalloc(T** p, size_t bytes) {
+  return hipMalloc((void**)p, bytes ? bytes : 16);
+}
+
+extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** out) {
+  if (!cfg || !out) return fail(FRN_EINVAL, "frn_create: null argument");
+  *out = nullptr;
+  const frn_config& c = *cfg;
+  if (!c.n_layers || !c.n_heads || !c.n_kv_heads || !c.hidden || !c.ffn || !c.head_dim || !c.vocab || !c.max_ctx)
+    return fail(FRN_EINVAL, "frn_create: zero dimension in config");
+  if (c.hidden % c.n_heads || c.hidden / c.n_heads != c.head_dim)
+    return fail(FRN_ESHAPE, "frn_create: head_dim %u != hidden %u / n_heads %u", c.head_dim, c.hidden, c.n_heads);
+  if (c.n_heads % c.n_kv_heads) return fail(FRN_ESHAPE, "frn_create: %u heads not divisible by %u kv heads", c.n_heads, c.n_kv_heads);
+  if (c.head_dim != 64 && c.head_dim != 128) return fail(FRN_ESHAPE, "frn_create: head_dim %u unsupported (64, 128)", c.head_dim);
+  if (c.n_heads / c.n_kv_heads > (c.head_dim == 64 ? 16u : 8u))
+    return fail(FRN_ESHAPE, "frn_create: %u query heads per kv head unsupported", c.n_heads / c.n_kv_heads);
+  if (c.hidden % 256 || c.ffn % 32) return fail(FRN_ESHAPE, "frn_create: hidden must be a multiple of 256, ffn of 32");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= device || device < 0)
+    return fail(FRN_ENODEV, "frn_create: no HIP device %d", device);
+  HIP_TRY(hipSetDevice(device), "hipSetDevice");
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(FRN_ENODEV, "frn_create: device %d is %s, this build targets gfx950", device, prop.gcnArchName);
+  frn_ctx* x = new frn_ctx();
+  x->cfg = c;
+  x->device = device;
+  size_t kvd = (size_t)c.n_kv_heads * c.head_dim, qd = (size_t)c.n_heads * c.head_dim;
+  size_t kv_bytes = (size_t)c.n_layers * c.max_ctx * kvd * 4;
+  hipError_t e;
+  if ((e = hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking)) || (e = dmalloc(&x->x, c.hidden * 4)) ||
+      (e = dmalloc(&x->q, qd * 4)) || (e = dmalloc(&x->k, kvd * 4)) || (e = dmalloc(&x->v, kvd * 4)) ||
+      (e = dmalloc(&x->att, qd * 4)) || (e = dmalloc(&x->act, (size_t)c.ffn * 4)) ||
+      (e = dmalloc(&x->logits, (size_t)c.vocab * 4)) ||
+      (e = dmalloc(&x->part, attention_part_floats(c.n_heads, c.head_dim, c.max_ctx) * 4)) ||
+      (e = dmalloc(&x->kcache, kv_bytes)) || (e = dmalloc(&x->vcache, kv_bytes)) ||
+      (e = dmalloc(&x->rope, (size_t)c.max_ctx * c.head_dim * 4)) || (e = dmalloc(&x->st, sizeof(StepState))) ||
+      (e = hipHostMalloc((void**)&x->h_st, sizeof(StepState), hipHostMallocDefault))) {
+    free_ctx(x);
+    return hip_fail(e, "frn_create: allocation");
+  }
+  // RoPE table (model.rs:207-210): freq = theta^(-2i/hd) via powf, angle in
+  // f32, sin/cos from the host libm -- the same calls the CPU path makes.
+  std::vector<float> tab((size_t)c.max_ctx * c.head_dim);
+  uint32_t half = c.head_dim / 2;
+  std::vector<float> freq(half);
+  for (uint32_t i = 0; i < half; ++i) freq[i] = powf(c.rope_theta, -2.0f * (float)i / (float)c.head_dim);
+  for (uint32_t p = 0; p < c.max_ctx; ++p)
+    for (uint32_t i = 0; i < half; ++i) {
+      volatile float angle = (float)p * freq[i];
+      tab[(size_t)p * c.head_dim + i] = cosf(angle);
+      tab[(size_t)p * c.head_dim + half + i] = sinf(angle);
+    }
+  StepState init{};
+  if ((e = hipMemcpy(x->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice)) ||
+      (e = hipMemcpy(x->st, &init, sizeof init, hipMemcpyHostToDevice)) ||
+      (e = hipMemset(x->kcache, 0, kv_bytes)) || (e = hipMemset(x->vcache, 0, kv_bytes)) ||
+      (e = gemv_prepare(c.hidden > c.ffn ? c.hidden : c.ffn))) {
+    free_ctx(x);
+    return hip_fail(e, "frn_create: init");
+  }
+  *out = x;
+  return FRN_OK;
+}
+
+extern "C" void frn_destroy(frn_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  free_ctx(ctx);
+}
+
+extern "C" frn_status frn_upload(frn_ctx* ctx, const char* name, uint32_t type, uint64_t out_dim, uint64_t in_dim,
+                                 const void* host, size_t bytes) {
+  if (!ctx || !name || (!host && bytes)) return fail(FRN_EINVAL, "frn_upload: null argument");
+  if (ctx->finalized) return fail(FRN_EINVAL, "frn_upload: context already finalized");
+  if (!known_type(type)) return fail(FRN_EDTYPE, "frn_upload: '%s' has ggml type %u without a kernel", name, type);
+  uint64_t n = out_dim * in_dim;
+  if (in_dim == 0 || out_dim == 0 || n % blk_elems(type))
+    return fail(FRN_ESHAPE, "frn_upload: '%s' has %llu elements, not a multiple of %d", name, (unsigned long long)n,
+                blk_elems(type));
+  if (type != T_F32 && in_dim % blk_elems(type))
+    return fail(FRN_ESHAPE, "frn_upload: '%s' in dim %llu not a multiple of %d", name, (unsigned long long)in_dim,
+                blk_elems(type));
+  size_t want = (size_t)(n / blk_elems(type)) * blk_bytes(type);
+  if (bytes != want)
+    return fail(FRN_ESHAPE, "frn_upload: '%s' is %zu bytes, expected %zu", name, bytes, want);
+  HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+  DevTensor t;
+  t.type = type;
+  t.out = out_dim;
+  t.in = in_dim;
+  bool vec = out_dim == 1;  // norms and biases: stored dequantized (Tensor::from_gguf)
+  t.bytes = vec ? (size_t)n * 4 : bytes;
+  // 256 B of slack: allocation granularity keeps tails readable by 16-byte loads
+  HIP_TRY(hipMalloc((void**)&t.ptr, t.bytes + 256), "frn_upload: hipMalloc");
+  hipError_t e = hipSuccess;
+  if (vec && type != T_F32) {
+    uint8_t* tmp = nullptr;
+    if (!(e = hipMalloc((void**)&tmp, bytes + 256)) && !(e = hipMemcpy(tmp, host, bytes, hipMemcpyHostToDevice)) &&
+        !(e = launch_dequant(type, tmp, n, (float*)t.ptr, ctx->stream)))
+      e = hipStreamSynchronize(ctx->stream);
+    if (tmp) (void)hipFree(tmp);
+    t.type = T_F32;
+  } else {
+    e = hipMemcpy(t.ptr, host, bytes, hipMemcpyHostToDevice);
+  }
+  if (e) {
+    (void)hipFree(t.ptr);
+    return hip_fail(e, "frn_upload: copy");
+  }
+  auto it = ctx->tensors.find(name);
+  if (it != ctx->tensors.end()) (void)hipFree(it->second.ptr);
+  ctx->tensors[name] = t;
+  return FRN_OK;
+}
+
+static frn_status need(frn_ctx* c, const std::string& name, uint64_t out, uint64_t in, bool matrix,
+                       const DevTensor** dst) {
+  auto it = c->tensors.find(name);
+  if (it == c->tensors.end()) return fail(FRN_EINVAL, "no tensor named '%s'", name.c_str());
+  const DevTensor& t = it->second;
+  if (t.out != out || t.in != in)
+    return fail(FRN_ESHAPE, "'%s' is [%llu, %llu], expected [%llu, %llu]", name.c_str(), (unsigned long long)t.out,
+                (unsigned long long)t.in, (unsigned long long)out, (unsigned long long)in);
+  if (matrix && t.type != T_F32 && (in % blk_elems(t.type)))
+    return fail(FRN_ESHAPE, "'%s' in dim not a multiple of the block", name.c_str());
+  *dst = &t;
+  return FRN_OK;
+}
+
+// Record one decode step on ctx->stream (under stream capture).
+static hipError_t record_step(frn_ctx* c, bool with_logits) {
+  const frn_config& g = c->cfg;
+  hipStream_t s = c->stream;
+  hipError_t e;
+  float scale = 1.0f / sqrtf((float)g.head_dim);  // model.rs:384
+  if ((e = launch_embed(c->embd->ptr, c->embd->type, g.hidden, (uint32_t)type_row_bytes(c->embd->type, g.hidden),
+                        c->st, c->x, s)))
+    return e;
+  for (uint32_t l = 0; l < g.n_layers; ++l) {
+    const LayerPtrs& L = c->layers[l];
+    auto gemv = [&](const DevTensor* w, const DevTensor* w2, const float* xin, const float* norm, const float* bias,
+                    float* out, GemvMode mode) {
+      GemvArgs a{};
+      a.w = w->ptr;
+      a.w2 = w2 ? w2->ptr : nullptr;
+      a.type = w->type;
+      a.rows = (uint32_t)w->out;
+      a.in = (uint32_t)w->in;
+      a.row_bytes = (uint32_t)type_row_bytes(w->type, w->in);
+      a.x = xin;
+      a.norm_w = norm;
+      a.eps = g.rms_eps;
+      a.bias = bias;
+      a.out = out;
+      a.state = c->st;
+      return launch_gemv(a, mode, s);
+    };
+    if ((e = gemv(L.wq, nullptr, c->x, L.attn_norm, L.bq, c->q, GEMV_STORE)) ||
+        (e = gemv(L.wk, nullptr, c->x, L.attn_norm, L.bk, c->k, GEMV_STORE)) ||
+        (e = gemv(L.wv, nullptr, c->x, L.attn_norm, L.bv, c->v, GEMV_STORE)))
+      return e;
+    size_t lo = (size_t)l * g.max_ctx * g.n_kv_heads * g.head_dim;
+    if ((e = launch_rope_kv(c->q, c->k, c->v, c->rope, g.n_heads, g.n_kv_heads, g.head_dim, c->kcache + lo,
+                            c->vcache + lo, c->st, s)))
+      return e;
+    if ((e = launch_attention(c->q, c->kcache + lo, c->vcache + lo, g.n_heads, g.n_kv_heads, g.head_dim, g.max_ctx,
+                              scale, c->part, c->att, c->st, s)))
+      return e;
+    if ((e = gemv(L.wo, nullptr, c->att, nullptr, nullptr, c->x, GEMV_RESID))) return e;
+    if ((e = gemv(L.gate, L.up, c->x, L.ffn_norm, nullptr, c->act, GEMV_SWIGLU))) return e;
+    if ((e = gemv(L.down, nullptr, c->act, nullptr, nullptr, c->x, GEMV_RESID))) return e;
+  }
+  if (with_logits) {
+    GemvArgs a{};
+    a.w = c->lm_head->ptr;
+    a.type = c->lm_head->type;
+    a.rows = g.vocab;
+    a.in = g.hidden;
+    a.row_bytes = (uint32_t)type_row_bytes(a.type, g.hidden);
+    a.x = c->x;
+    a.norm_w = c->out_norm;
+    a.eps = g.rms_eps;
+    a.out = c->logits;
+    a.state = c->st;
+    if ((e = launch_gemv(a, GEMV_ARGMAX, s))) return e;
+  }
+  return launch_step_end(c->st, with_logits ? 1 : 0, s);
+}
+
+static frn_status capture(frn_ctx* c, bool with_logits, hipGraph_t* graph, hipGraphExec_t* exec) {
+  HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  hipError_t e = record_step(c, with_logits);
+  hipGraph_t gr = nullptr;
+  hipError_t e2 = hipStreamEndCapture(c->stream, &gr);
+  if (e) {
+    if (gr) hipGraphDestroy(gr);
+    return hip_fail(e, "recording decode step");
+  }
+  if (e2) return hip_fail(e2, "hipStreamEndCapture");
+  *graph = gr;
+  HIP_TRY(hipGraphInstantiate(exec, gr, nullptr, nullptr, 0), "hipGraphInstantiate");
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_finalize(frn_ctx* c) {
+  if (!c) return fail(FRN_EINVAL, "frn_finalize: null context");
+  if (c->finalized) return FRN_OK;
+  const frn_config& g = c->cfg;
+  uint64_t H = g.hidden, qd = (uint64_t)g.n_heads * g.head_dim, kd = (uint64_t)g.n_kv_heads * g.head_dim;
+  frn_status st;
+  const DevTensor* t;
+  // Model::load's tensor set (model.rs:147-161, 522-545)
+  if ((st = need(c, "token_embd.weight", g.vocab, H, true, &c->embd))) return st;
+  if ((st = need(c, "output_norm.weight", 1, H, false, &t))) return st;
+  c->out_norm = (const float*)t->ptr;
+  if (c->tensors.count("output.weight")) {
+    if ((st = need(c, "output.weight", g.vocab, H, true, &c->lm_head))) return st;
+  } else {
+    c->lm_head = c->embd;
+  }
+  c->layers.resize(g.n_layers);
+  char nm[96];
+  for (uint32_t l = 0; l < g.n_layers; ++l) {
+    LayerPtrs& L = c->layers[l];
+    auto vec = [&](const char* suf, uint64_t n, const float** dst) {
+      snprintf(nm, sizeof nm, "blk.%u.%s", l, suf);
+      const DevTensor* tt;
+      frn_status s2 = need(c, nm, 1, n, false, &tt);
+      if (!s2) *dst = (const float*)tt->ptr;
+      return s2;
+    };
+    auto mat = [&](const char* suf, uint64_t o, uint64_t i, const DevTensor** dst) {
+      snprintf(nm, sizeof nm, "blk.%u.%s", l, suf);
+      return need(c, nm, o, i, true, dst);
+    };
+    if ((st = vec("attn_norm.weight", H, &L.attn_norm)) || (st = mat("attn_q.weight", qd, H, &L.wq)) ||
+        (st = vec("attn_q.bias", qd, &L.bq)) || (st = mat("attn_k.weight", kd, H, &L.wk)) ||
+        (st = vec("attn_k.bias", kd, &L.bk)) || (st = mat("attn_v.weight", kd, H, &L.wv)) ||
+        (st = vec("attn_v.bias", kd, &L.bv)) || (st = mat("attn_output.weight", H, qd, &L.wo)) ||
+        (st = vec("ffn_norm.weight", H, &L.ffn_norm)) || (st = mat("ffn_gate.weight", g.ffn, H, &L.gate)) ||
+        (st = mat("ffn_up.weight", g.ffn, H, &L.up)) || (st = mat("ffn_down.weight", H, g.ffn, &L.down)))
+      return st;
+    if (L.gate->type != L.up->type)
+      return fail(FRN_EDTYPE, "blk.%u: ffn_gate and ffn_up must share a type for the fused SwiGLU kernel", l);
+  }
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  if ((st = capture(c, true, &c->graph_step, &c->g_step))) return st;
+  if ((st = capture(c, false, &c->graph_prefill, &c->g_prefill))) return st;
+  c->finalized = true;
+  return FRN_OK;
+}
+
+// Run one position with token `tok` (already validated); with_logits picks
+// the graph that ends in lm_head + argmax.
+static frn_status run_step(frn_ctx* c, uint32_t tok, bool with_logits) {
+  if (tok != c->last_next) {
+    c->h_st->tok = tok;
+    HIP_TRY(hipMemcpyAsync((char*)c->st + offsetof(StepState, tok), &c->h_st->tok, 4, hipMemcpyHostToDevice, c->stream),
+            "token upload");
+  }
+  HIP_TRY(hipGraphLaunch(with_logits ? c->g_step : c->g_prefill, c->stream), "hipGraphLaunch");
+  c->len += 1;
+  c->last_next = 0xFFFFFFFFu;
+  return FRN_OK;
+}
+
+static frn_status check_ready(frn_ctx* c, uint32_t n) {
+  if (!c) return fail(FRN_EINVAL, "null context");
+  if (!c->finalized) return fail(FRN_EINVAL, "context not finalized");
+  if ((uint64_t)c->len + n > c->cfg.max_ctx)
+    return fail(FRN_ECTX_OVERFLOW, "context overflow: %u + %u > max_ctx %u", c->len, n, c->cfg.max_ctx);
+  return FRN_OK;
+}
+
+static frn_status read_next(frn_ctx* c, uint32_t* next_id) {
+  HIP_TRY(hipMemcpyAsync(&c->h_st->next_tok, (char*)c->st + offsetof(StepState, next_tok), 4, hipMemcpyDeviceToHost,
+                         c->stream),
+          "next-id read-back");
+  HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  c->last_next = c->h_st->next_tok;
+  c->have_logits = true;
+  if (next_id) *next_id = c->last_next;
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_prefill(frn_ctx* c, const uint32_t* ids, uint32_t n, uint32_t* next_id) {
+  frn_status st;
+  if ((st = check_ready(c, n))) return st;
+  if (!ids || n == 0) return fail(FRN_EINVAL, "frn_prefill: empty prompt");
+  for (uint32_t i = 0; i < n; ++i)
+    if (ids[i] >= c->cfg.vocab) return fail(FRN_ETOKEN, "token id %u out of range (vocab %u)", ids[i], c->cfg.vocab);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  c->last_next = 0xFFFFFFFFu;
+  for (uint32_t i = 0; i < n; ++i) {
+    // per-position token upload: make sure the previous copy has landed
+    if (i) HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if ((st = run_step(c, ids[i], i + 1 == n))) return st;
+  }
+  return read_next(c, next_id);
+}
+
+extern "C" frn_status frn_decode(frn_ctx* c, uint32_t id, uint32_t* next_id) {
+  frn_status st;
+  if ((st = check_ready(c, 1))) return st;
+  if (id >= c->cfg.vocab) return fail(FRN_ETOKEN, "token id %u out of range (vocab %u)", id, c->cfg.vocab);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  uint32_t prev = c->last_next;
+  c->last_next = prev;  // run_step skips the upload when id is the device's own argmax
+  if ((st = run_step(c, id, true))) return st;
+  return read_next(c, next_id);
+}
+
+extern "C" frn_status frn_logits(frn_ctx* c, float* host_out, size_t n) {
+  if (!c || !host_out) return fail(FRN_EINVAL, "frn_logits: null argument");
+  if (!c->have_logits) return fail(FRN_EINVAL, "frn_logits: no logits yet");
+  if (n < c->cfg.vocab) return fail(FRN_EINVAL, "frn_logits: buffer holds %zu < vocab %u", n, c->cfg.vocab);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  HIP_TRY(hipMemcpyAsync(host_out, c->logits, (size_t)c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->stream), "logits copy");
+  HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_reset(frn_ctx* c) {
+  if (!c) return fail(FRN_EINVAL, "frn_reset: null context");
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  StepState init{};
+  HIP_TRY(hipMemcpy(c->st, &init, sizeof init, hipMemcpyHostToDevice), "state reset");
+  c->len = 0;
+  c->last_next = 0xFFFFFFFFu;
+  c->have_logits = false;
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_cache_len(frn_ctx* c, uint32_t* len) {
+  if (!c || !len) return fail(FRN_EINVAL, "frn_cache_len: null argument");
+  *len = c->len;
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_cache_read(frn_ctx* c, uint32_t layer, uint32_t which, uint32_t n, float* host_out) {
+  if (!c || !host_out) return fail(FRN_EINVAL, "frn_cache_read: null argument");
+  if (layer >= c->cfg.n_layers || n > c->cfg.max_ctx || which > 1) return fail(FRN_EINVAL, "frn_cache_read: out of range");
+  size_t kvd = (size_t)c->cfg.n_kv_heads * c->cfg.head_dim;
+  const float* src = (which ? c->vcache : c->kcache) + (size_t)layer * c->cfg.max_ctx * kvd;
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  HIP_TRY(hipMemcpy(host_out, src, (size_t)n * kvd * 4, hipMemcpyDeviceToHost), "cache copy");
+  return FRN_OK;
+}
+
+// ---- --timings (perf.rs) -----------------------------------------------------
+extern "C" frn_status frn_timings_enable(frn_ctx* c, int enable) {
+  if (!c) return fail(FRN_EINVAL, "null context");
+  c->timing = enable != 0;
+  return FRN_OK;
+}
+extern "C" frn_status frn_timings_reset(frn_ctx* c) {
+  if (!c) return fail(FRN_EINVAL, "null context");
+  memset(c->t_ms, 0, sizeof c->t_ms);
+  memset(c->t_calls, 0, sizeof c->t_calls);
+  return FRN_OK;
+}
+extern "C" frn_status frn_timings(frn_ctx* c, frn_timing* out, uint32_t max, uint32_t* n) {
+  static const char* names[9] = {"matmul", "rmsnorm", "softmax", "rope", "attn scores", "attn apply", "add/swiglu", "embed", "sample"};
+  if (!c || !n) return fail(FRN_EINVAL, "null argument");
+  uint32_t k = 0;
+  for (int i = 0; i < 9 && k < max; ++i) {
+    snprintf(out[k].name, sizeof out[k].name, "%s", names[i]);
+    out[k].ms = c->t_ms[i];
+    out[k].calls = c->t_calls[i];
+    ++k;
+  }
+  *n = k;
+  return FRN_OK;
+}
+
+// ---- single-op entry points ------------------------------------------------------
+extern "C" frn_status frn_dequant(uint32_t type, const void* raw_dev, size_t raw_bytes, size_t n, float* out_dev,
+                                  void* stream) {
+  if (!known_type(type)) return fail(FRN_EDTYPE, "dequantization for type %u is not implemented", type);
+  if (n % blk_elems(type)) return fail(FRN_ESHAPE, "element count %zu is not a multiple of %d", n, blk_elems(type));
+  size_t want = n / blk_elems(type) * blk_bytes(type);
+  if (raw_bytes != want)
+    return fail(FRN_ESHAPE, "data is %zu bytes, expected %zu (%zu blocks of %d)", raw_bytes, want,
+                n / blk_elems(type), blk_bytes(type));
+  if (n && (!raw_dev || !out_dev)) return fail(FRN_EINVAL, "frn_dequant: null pointer");
+  HIP_TRY(launch_dequant(type, (const uint8_t*)raw_dev, n, out_dev, (hipStream_t)stream), "dequant launch");
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_matmul_quant(uint32_t type, const void* w_dev, size_t w_bytes, const float* a_dev,
+                                       uint32_t seq, float* out_dev, uint32_t d_out, uint32_t d_in, void* stream) {
+  if (!known_type(type)) return fail(FRN_EDTYPE, "no fused matmul kernel for type %u", type);
+  if (type != T_F32 && d_in % blk_elems(type))
+    return fail(FRN_ESHAPE, "matmul: in dim %u not a multiple of %d", d_in, blk_elems(type));
+  if (d_in % 32) return fail(FRN_ESHAPE, "matmul: in dim %u not a multiple of 32", d_in);
+  size_t want = (size_t)d_out * type_row_bytes(type, d_in);
+  if (w_bytes != want) return fail(FRN_ESHAPE, "matmul: bad weight byte count %zu, expected %zu", w_bytes, want);
+  if (!w_dev || !a_dev || !out_dev) return fail(FRN_EINVAL, "frn_matmul_quant: null pointer");
+  // the kernels use 16-byte loads of rows and of the activation vector
+  if (((uintptr_t)w_dev | (uintptr_t)a_dev) & 15)
+    return fail(FRN_EINVAL, "frn_matmul_quant: w_dev and a_dev must be 16-byte aligned");
+  if (gemv_lds_bytes(type, d_in) > 160 * 1024)
+    return fail(FRN_ESHAPE, "matmul: in dim %u exceeds the 160 KiB LDS staging limit", d_in);
+  if (seq == 0 || d_out == 0) return FRN_OK;
+  static uint32_t prepared = 0;
+  if (d_in > prepared) {
+    HIP_TRY(gemv_prepare(d_in), "gemv_prepare");
+    prepared = d_in;
+  }
+  for (uint32_t s = 0; s < seq; ++s) {
+    GemvArgs a{};
+    a.w = (const uint8_t*)w_dev;
+    a.type = type;
+    a.rows = d_out;
+    a.in = d_in;
+    a.row_bytes = (uint32_t)type_row_bytes(type, d_in);
+    a.x = a_dev + (size_t)s * d_in;
+    a.out = out_dev + (size_t)s * d_out;
+    HIP_TRY(launch_gemv(a, GEMV_STORE, (hipStream_t)stream), "gemv launch");
+  }
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_argmax(const float* x_dev, size_t n, uint32_t* out_dev, void* stream) {
+  if (!x_dev || !out_dev || n == 0) return fail(FRN_EINVAL, "frn_argmax: bad argument");
+  static thread_local uint64_t* scratch = nullptr;
+  if (!scratch) HIP_TRY(hipMalloc((void**)&scratch, 256), "argmax scratch");
+  HIP_TRY(launch_argmax(x_dev, n, scratch, out_dev, (hipStream_t)stream), "argmax launch");
+  return FRN_OK;
+}

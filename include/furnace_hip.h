@@ -1,0 +1,141 @@
+/*
+ * furnace_hip.h -- C ABI of the MI355X (gfx950) token-loop engine.
+ *
+ * This is the drop-in boundary for furnace's decode/prefill path.  furnace
+ * (Rust) keeps its host code -- GGUF mmap parsing, tokenizer, sampler, the
+ * generate loop and CLI -- and replaces everything below `generate`'s calls
+ * to Model::forward_cached + Sampler::sample with these entry points.
+ * Plain C types only (fixed-width integers, float, pointers, sizes), so a
+ * Rust `extern "C"` block binds them unchanged.
+ *
+ * Conventions
+ *  - Every entry point returns frn_status (0 = success) and never aborts.
+ *    The message for the last failure on the calling thread is
+ *    frn_last_error().
+ *  - A context is single-threaded: the caller serialises calls on it.
+ *  - One HIP stream per context.  frn_decode's only host synchronisation is
+ *    the 4-byte read-back of the next token id.
+ *  - Quantized weights are uploaded once in their raw GGUF block layout
+ *    (Q8_0 34 B / 32, Q5_0 22 B / 32, Q4_K 144 B / 256, Q6_K 210 B / 256);
+ *    full-precision copies of them never exist on the device.
+ */
+#ifndef FURNACE_HIP_H
+#define FURNACE_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum frn_status {
+  FRN_OK = 0,
+  FRN_EINVAL = 1,        /* bad argument, missing tensor, wrong call order */
+  FRN_EDTYPE = 2,        /* ggml type without a kernel (quant.rs:191, :279) */
+  FRN_ESHAPE = 3,        /* shape/byte-count mismatch (quant.rs:18-32, :210-212) */
+  FRN_ECTX_OVERFLOW = 4, /* start + n > max_ctx (model.rs:581-585, :348-352) */
+  FRN_ETOKEN = 5,        /* token id >= vocab (model.rs:489) */
+  FRN_EOOM = 6,          /* device allocation failed */
+  FRN_EHIP = 7,          /* any other HIP runtime error */
+  FRN_ENODEV = 8         /* no usable gfx950 device */
+} frn_status;
+
+/* ggml tensor type codes, src/gguf.rs:180-201 (the subset with kernels). */
+enum { FRN_TYPE_F32 = 0, FRN_TYPE_Q5_0 = 6, FRN_TYPE_Q8_0 = 8, FRN_TYPE_Q4_K = 12, FRN_TYPE_Q6_K = 14 };
+
+/* Model configuration: src/model.rs:26-38 Config, filled by the host from
+ * GGUF metadata exactly as Config::from_gguf (model.rs:41-60) does.
+ * max_ctx replaces KvCache::new's max_ctx (model.rs:330; generate.rs:91). */
+typedef struct frn_config {
+  uint32_t n_layers, n_heads, n_kv_heads, hidden, ffn, head_dim, vocab, max_ctx;
+  float rope_theta, rms_eps;
+  uint32_t tied_lm_head; /* 1 when output.weight is absent (model.rs:541-545) */
+  uint32_t reserved;
+} frn_config;
+
+typedef struct frn_ctx frn_ctx;
+
+/* Allocate a context on HIP device `device`: the KV cache (f32,
+ * [n_layers][max_ctx][n_kv_heads*head_dim] for K and V, model.rs:321-339),
+ * activation buffers and the RoPE table.  Replaces Model::load's allocation
+ * side (model.rs:520-552) and KvCache::new (model.rs:330-339). */
+frn_status frn_create(const frn_config* cfg, int device, frn_ctx** out);
+
+/* Copy one GGUF tensor from host memory (e.g. the mmap) to HBM, raw.
+ * `name` is the GGUF tensor name ("token_embd.weight", "blk.3.ffn_up.weight",
+ * "output_norm.weight", ...); out_dim/in_dim are dims[1]/dims[0] (ggml order,
+ * model.rs:123-124; 1-D tensors pass out_dim = 1).  The host may unmap the
+ * source after the call.  Replaces load_weight / Tensor::from_gguf
+ * (model.rs:112-126, tensor.rs:55-60). */
+frn_status frn_upload(frn_ctx* ctx, const char* name, uint32_t ggml_type, uint64_t out_dim, uint64_t in_dim,
+                      const void* host, size_t bytes);
+
+/* Check that every tensor Model::load requires is present and
+ * consistently shaped, then build the decode step.  Must follow the uploads
+ * and precede prefill/decode. */
+frn_status frn_finalize(frn_ctx* ctx);
+
+/* Model::forward_cached(&prompt) + Sampler::sample at temperature 0
+ * (model.rs:579-592, sampler.rs:91-94, generate.rs:69-77): runs the n ids at
+ * positions ctx.len .. ctx.len+n, advances ctx.len by n and writes the
+ * argmax of the last position's logits (first maximum on ties). */
+frn_status frn_prefill(frn_ctx* ctx, const uint32_t* ids, uint32_t n, uint32_t* next_id);
+
+/* One decode step: Model::forward_cached(&[id]) + argmax
+ * (generate.rs:136, :124).  Only the next id crosses back to the host. */
+frn_status frn_decode(frn_ctx* ctx, uint32_t id, uint32_t* next_id);
+
+/* Copy the last step's logits [vocab] to host memory (the 1e-3 parity gate
+ * and any host-side sampler).  n must be >= vocab. */
+frn_status frn_logits(frn_ctx* ctx, float* host_out, size_t n);
+
+/* Forget the cached positions (ctx.len = 0).  Weights stay resident. */
+frn_status frn_reset(frn_ctx* ctx);
+/* Current number of cached positions (KvCache::len, model.rs:324). */
+frn_status frn_cache_len(frn_ctx* ctx, uint32_t* len);
+/* Read layer `layer`'s cached K (which = 0) or V (which = 1) rows [0, n)
+ * into host memory, n * n_kv_heads * head_dim floats (debug/parity). */
+frn_status frn_cache_read(frn_ctx* ctx, uint32_t layer, uint32_t which, uint32_t n, float* host_out);
+
+void frn_destroy(frn_ctx* ctx);
+
+/* Message for the last failure on this thread ("" if none). */
+const char* frn_last_error(void);
+
+/* --timings dashboard (perf.rs:25-96): per-category GPU time of the decode
+ * steps since the last frn_timings_reset, measured with HIP events around
+ * each kernel when enabled.  Categories follow perf.rs's counters
+ * (matmul, rmsnorm, softmax, rope, attn scores, attn apply, add/swiglu,
+ * embed, sample); kernels that fuse several ops report under the op that
+ * dominates their bytes. */
+typedef struct frn_timing {
+  char name[16];
+  double ms;
+  uint64_t calls;
+} frn_timing;
+frn_status frn_timings_enable(frn_ctx* ctx, int enable);
+frn_status frn_timings_reset(frn_ctx* ctx);
+frn_status frn_timings(frn_ctx* ctx, frn_timing* out, uint32_t max, uint32_t* n);
+
+/* ---- single-op entry points (device pointers, caller's stream) ----------- */
+
+/* quant::dequantize (quant.rs:261-281) on device buffers: n_elems values of
+ * `type` from raw_dev (raw_bytes long) into out_dev as f32.  Bit-exact with
+ * the CPU path.  stream may be NULL (the default stream). */
+frn_status frn_dequant(uint32_t type, const void* raw_dev, size_t raw_bytes, size_t n_elems, float* out_dev,
+                       void* stream);
+
+/* quant::matmul_quant (quant.rs:170-193): a_dev [seq, d_in] f32 times the
+ * raw quantized weight w_dev [d_out, d_in] -> out_dev [seq, d_out] f32.
+ * seq == 1 runs the decode GEMV kernel for `type`; seq > 1 the prefill
+ * kernel.  w_bytes must equal d_out * (d_in / block) * block_bytes. */
+frn_status frn_matmul_quant(uint32_t type, const void* w_dev, size_t w_bytes, const float* a_dev, uint32_t seq,
+                            float* out_dev, uint32_t d_out, uint32_t d_in, void* stream);
+
+/* Device argmax over n floats, first maximum on ties (generate.rs:69-77). */
+frn_status frn_argmax(const float* x_dev, size_t n, uint32_t* out_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

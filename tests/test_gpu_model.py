@@ -1,0 +1,111 @@
+"""End-to-end parity of the device token loop against the oracle on seeded
+synthetic GGUF models: last-position logits within 1e-3 max-abs, KV cache
+rows, and greedy (temperature 0) ids identical for the first 32 tokens."""
+import os
+
+import numpy as np
+import pytest
+
+import furnace_amd as fa
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 1e-3  # max-abs on last-position logits
+N_IDS = 32        # greedy ids that must match exactly
+
+
+def small_models():
+    return {
+        "tiny-q4_k_m": dict(n_layers=3, n_heads=4, n_kv_heads=2, hidden=256, ffn=512, vocab=3000, mix=fa.MIX_Q4_K_M,
+                            tied=1, embd_type=fa.Q6_K, output_type=fa.Q6_K),
+        "tiny-q8_0-hd64": dict(n_layers=2, n_heads=4, n_kv_heads=1, hidden=256, ffn=256 + 32, vocab=2000,
+                               mix=fa.MIX_ALL_Q8_0, tied=1, embd_type=fa.Q8_0, output_type=fa.Q8_0),
+        "tiny-q5_0-untied": dict(n_layers=2, n_heads=2, n_kv_heads=2, hidden=256, ffn=512, vocab=1000,
+                                 mix=fa.MIX_ALL_Q5_0, tied=0, embd_type=fa.Q5_0, output_type=fa.Q8_0),
+        "tiny-q4_k-gq8": dict(n_layers=2, n_heads=8, n_kv_heads=1, hidden=1024, ffn=768, vocab=500,
+                              mix=fa.MIX_ALL_Q4_K, tied=1, embd_type=fa.Q4_K, output_type=fa.Q4_K),
+    }
+
+
+@pytest.mark.parametrize("name", list(small_models()))
+def test_small_model_prefill_decode(hip, tmpdir_models, name):
+    path = os.path.join(tmpdir_models, name + ".gguf")
+    fa.synth_write(path, seed=17, **small_models()[name])
+    rng = np.random.default_rng(5)
+    cfg = small_models()[name]
+    prompt = rng.integers(0, cfg["vocab"], 300 if name == "tiny-q4_k-gq8" else 9).astype(np.uint32)
+    print("model %s prompt %d" % (name, prompt.size), flush=True)
+    ref = orc.Model(path)
+    ref.new_cache(512)
+    ref_logits = ref.forward_cached(prompt)
+    m = fa.Model(path, max_ctx=512)
+    nxt = m.prefill(prompt)
+    got = m.logits()
+    assert np.max(np.abs(got - ref_logits)) <= LOGIT_TOL
+    assert nxt == orc.argmax(got)
+    assert m.cache_len() == prompt.size
+    for layer in (0, cfg["n_layers"] - 1):
+        for which in (0, 1):
+            gk = m.cache_read(layer, which, prompt.size)
+            rk = ref.cache_read(layer, which, prompt.size)
+            assert np.max(np.abs(gk - rk)) <= 1e-4 * max(1.0, float(np.abs(rk).max()))
+    # greedy decode, step by step against the oracle's logits
+    tok = orc.argmax(ref_logits)
+    assert tok == nxt
+    for step in range(6):
+        ref_logits = ref.forward_cached([tok])
+        nxt = m.decode(tok)
+        got = m.logits()
+        assert np.max(np.abs(got - ref_logits)) <= LOGIT_TOL, step
+        assert nxt == orc.argmax(ref_logits), step
+        tok = nxt
+    m.close()
+    ref.close()
+
+
+def test_errors_from_the_device_context(hip, tmpdir_models):
+    path = os.path.join(tmpdir_models, "err.gguf")
+    fa.synth_write(path, seed=2, **small_models()["tiny-q4_k_m"])
+    m = fa.Model(path, max_ctx=8)
+    with pytest.raises(fa.FrnError) as e:
+        m.prefill([3000])  # vocab is 3000
+    assert e.value.status == 5
+    with pytest.raises(fa.FrnError) as e:
+        m.prefill(list(range(9)))
+    assert e.value.status == 4
+    m.prefill(list(range(8)))
+    with pytest.raises(fa.FrnError) as e:
+        m.decode(1)
+    assert e.value.status == 4
+    m.reset()
+    assert m.cache_len() == 0
+    m.prefill([1, 2])
+    m.close()
+
+
+def _greedy_parity(path, prompt, max_new, max_ctx):
+    ref = orc.Model(path)
+    ref_ids, _, ref_last = ref.generate_greedy(prompt, max_new, max_ctx)
+    ref.close()
+    m = fa.Model(path, max_ctx=max_ctx)
+    ids, st = m.generate_greedy(prompt, max_new)
+    got_last = m.logits()
+    m.close()
+    return ids, ref_ids, got_last, ref_last
+
+
+@pytest.mark.parametrize("preset,n_prompt", [("qwen2-0.5b-q8_0", 16), ("qwen2-1.5b-q4_k_m", 128)])
+def test_full_model_greedy_ids_and_logits(hip, tmpdir_models, preset, n_prompt):
+    path = os.path.join(tmpdir_models, preset + ".gguf")
+    print("writing %s" % preset, flush=True)
+    fa.synth_write(path, seed=0xF0E1, **fa.PRESETS[preset])
+    prompt = np.random.default_rng(0xF0E1).integers(0, 151643, n_prompt).astype(np.uint32)
+    orc.set_threads(min(16, os.cpu_count() or 1))
+    print("running %s prompt %d" % (preset, n_prompt), flush=True)
+    ids, ref_ids, got_last, ref_last = _greedy_parity(path, prompt, N_IDS + 1, 512)
+    print("gpu ids", ids[:N_IDS], flush=True)
+    print("ref ids", ref_ids[:N_IDS], flush=True)
+    assert ids[:N_IDS] == ref_ids[:N_IDS]
+    assert np.max(np.abs(got_last - ref_last)) <= LOGIT_TOL
+    os.remove(path)
