@@ -1,0 +1,203 @@
+#!/usr/bin/env python3
+"""Decode throughput of the MI355X token loop on the Qwen2-1.5B-shaped Q4_K_M
+synthetic model (128-token random prompt, greedy decode), plus the fraction
+of the 8 TB/s HBM roofline it reaches.
+
+One step = one decode forward (embedding, 28 layers, lm_head, argmax) for one
+token, with the weights already resident in HBM.  Prints one JSON line.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+import furnace_amd as fa  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tokens/s + % of HBM peak (Qwen2-1.5B-shape Q4_K_M, 1 GPU)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def tensor_bytes(gguf, name):
+    t, nd, p, b = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_void_p(), ctypes.c_size_t()
+    dims = (ctypes.c_uint64 * 4)()
+    fa.check(fa.load().frn_gguf_tensor(gguf, name.encode(), ctypes.byref(t), dims, ctypes.byref(nd),
+                                       ctypes.byref(p), ctypes.byref(b)))
+    return b.value, t.value
+
+
+def algorithmic_bytes(model):
+    """Bytes one decode step must move at minimum: every weight once
+    (quantized size), norms and biases, one embedding row, the lm_head, and
+    per attended position 2 * L * kv_dim * 4 bytes of f32 KV cache."""
+    c = model.cfg
+    g = model.gguf
+    w = 0
+    per = {}
+    for l in range(c.n_layers):
+        for n in ("attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight", "ffn_gate.weight",
+                  "ffn_up.weight", "ffn_down.weight", "attn_norm.weight", "ffn_norm.weight", "attn_q.bias",
+                  "attn_k.bias", "attn_v.bias"):
+            b, _ = tensor_bytes(g, "blk.%d.%s" % (l, n))
+            w += b
+            per.setdefault(n, []).append(b)
+    eb, et = tensor_bytes(g, "token_embd.weight")
+    w += eb // c.vocab  # one row
+    w += tensor_bytes(g, "output_norm.weight")[0]
+    lm = tensor_bytes(g, "output.weight")[0] if not c.tied_lm_head else eb
+    w += lm
+    kv_per_pos = 2 * c.n_layers * c.n_kv_heads * c.head_dim * 4
+    return w, kv_per_pos, per, lm
+
+
+def cpu_baseline(path, prompt, budget_s, threads):
+    """The oracle (plain-C restatement of furnace's CPU path) on the host
+    cores: an 8-token prefill of the same model, then greedy decode steps
+    until about budget_s of decode work."""
+    from oracle import oracle as orc
+    orc.set_threads(threads)
+    m = orc.Model(path)
+    m.new_cache(512)
+    t0 = time.perf_counter()
+    logits = m.forward_cached(prompt[:8])
+    prefill_s = time.perf_counter() - t0
+    tok = orc.argmax(logits)
+    steps, dec = 0, 0.0
+    while dec < budget_s and steps < 256:
+        t1 = time.perf_counter()
+        logits = m.forward_cached([tok])
+        dec += time.perf_counter() - t1
+        tok = orc.argmax(logits)
+        steps += 1
+    m.close()
+    return steps / dec, steps, dec, prefill_s
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=255, help="timed decode steps (256-token decode = 255 forwards)")
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--model", default="qwen2-1.5b-q4_k_m", choices=sorted(fa.PRESETS))
+    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--seed", type=int, default=0xF0E1)
+    ap.add_argument("--timing-steps", type=int, default=32, help="eager steps with per-kernel events")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gguf", default=None, help="use this GGUF instead of writing the synthetic one")
+    ap.add_argument("--eager", action="store_true", help="launch kernels one by one (for profilers) instead of "
+                    "replaying the captured decode graph")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this engine runs on one GPU; --gpus %d is not supported (sharding is design-only)" %
+              args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    tmp = tempfile.mkdtemp(prefix="frn_bench_")
+    path = args.gguf or os.path.join(tmp, args.model + ".gguf")
+    if not args.gguf:
+        t0 = time.perf_counter()
+        fa.synth_write(path, seed=args.seed, threads=min(16, os.cpu_count() or 1), **fa.PRESETS[args.model])
+        log("synthetic %s written in %.1f s" % (args.model, time.perf_counter() - t0))
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, 151643, args.prompt).astype(np.uint32)
+    max_ctx = args.prompt + args.steps + args.timing_steps + max(args.warmup, 8) + 2
+
+    t0 = time.perf_counter()
+    model = fa.Model(path, max_ctx=max_ctx, eager=args.eager)
+    log("weights uploaded in %.2f s" % (time.perf_counter() - t0))
+    w_bytes, kv_per_pos, per, lm_bytes = algorithmic_bytes(model)
+    hip = fa.Hip()
+
+    # warm-up: compile caches, first graph launches
+    tok = model.prefill(prompt[:8])
+    for _ in range(args.warmup):
+        tok = model.decode(tok)
+    model.reset()
+
+    # prefill of the whole prompt, then the timed decode steps
+    hip.sync()
+    t0 = time.perf_counter()
+    tok = model.prefill(prompt)
+    hip.sync()
+    prefill_s = time.perf_counter() - t0
+    hip.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tok = model.decode(tok)
+    hip.sync()
+    dec_s = time.perf_counter() - t0
+    ms_per_step = dec_s * 1000.0 / args.steps
+    # positions attended by the timed steps: prompt+1 .. prompt+steps
+    avg_attended = args.prompt + (args.steps + 1) / 2.0
+    step_bytes = w_bytes + kv_per_pos * avg_attended
+    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log("decode: %d steps, %.4f ms/token, %.1f tokens/s, %.1f GB/s (%.1f%% of HBM peak)" %
+        (args.steps, ms_per_step, 1000 / ms_per_step, step_gbs, 100 * step_gbs / HBM_PEAK_GBS))
+    log("prefill: %d tokens in %.3f s (%.1f tokens/s)" % (args.prompt, prefill_s, args.prompt / prefill_s))
+
+    # live per-kernel durations (HIP events around each kernel, eager steps)
+    model.timings_reset()
+    model.timings_enable(True)
+    for _ in range(args.timing_steps):
+        tok = model.decode(tok)
+    model.timings_enable(False)
+    tm = model.timings()
+    c = model.cfg
+    log("per-kernel (eager, %d steps):" % args.timing_steps)
+    for k, (ms, calls) in tm.items():
+        if calls:
+            log("  %-10s %9.3f ms  %6d calls  %8.2f us/call" % (k, ms, calls, 1000 * ms / calls))
+    # dominant kernel: the fused gate/up GEMV + SwiGLU (largest share of time)
+    gu_ms, gu_calls = tm["gate_up"]
+    gu_bytes = (sum(per["ffn_gate.weight"]) + sum(per["ffn_up.weight"])) / c.n_layers + 4 * (c.hidden + c.ffn)
+    gu_avg_s = gu_ms * 1e-3 / gu_calls
+    gu_gbs = gu_bytes / gu_avg_s / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        tps, steps, dec, pf = cpu_baseline(path, prompt, args.cpu_seconds, threads)
+        log("cpu baseline: %.2f tokens/s (%d decode steps in %.1f s, %d threads; 8-token prefill %.1f s)" %
+            (tps, steps, dec, threads, pf))
+        cpu = {"value": round(tps, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "sample": "oracle (C restatement of furnace's CPU path) on the same %s GGUF: 8-token prefill, "
+                         "then %d greedy decode steps" % (args.model, steps)}
+    model.close()
+    if not args.gguf:
+        os.remove(path)
+        os.rmdir(tmp)
+
+    out = {
+        "metric": METRIC, "value": round(1000.0 / ms_per_step, 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights, uniform random prompt ids)",
+        "config": {"workload": "%s greedy decode after a %d-token prompt" % (args.model, args.prompt),
+                   "weights": "Q4_K_M mix (Q4_K; Q6_K attn_v/ffn_down on even layers; Q6_K tied lm_head)"
+                   if "q4_k_m" in args.model else "Q8_0", "prompt_tokens": args.prompt,
+                   "decode_tokens": args.steps, "bytes_per_token": int(step_bytes),
+                   "hbm_frac_per_token": round(step_gbs / HBM_PEAK_GBS, 4),
+                   "prefill_tokens_per_s": round(args.prompt / prefill_s, 1)},
+        "roofline": {"bound": "hbm", "kernel": "gate_up (fused Q4_K gate+up GEMV + SwiGLU)",
+                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": int(gu_bytes), "avg_us": round(gu_avg_s * 1e6, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

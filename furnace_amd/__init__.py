@@ -18,6 +18,8 @@ CLI_PATH = os.path.join(_PKG, "bin", "furnace-hip")
 F32, Q5_0, Q8_0, Q4_K, Q6_K = 0, 6, 8, 12, 14
 BLOCK = {F32: (1, 4), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 
+FLAG_EAGER = 1  # FRN_FLAG_EAGER
+
 MIX_ALL_Q8_0, MIX_Q4_K_M, MIX_ALL_Q4_K, MIX_ALL_Q6_K, MIX_ALL_Q5_0, MIX_ALL_F32 = range(6)
 
 STATUS = {0: "FRN_OK", 1: "FRN_EINVAL", 2: "FRN_EDTYPE", 3: "FRN_ESHAPE", 4: "FRN_ECTX_OVERFLOW",
@@ -34,7 +36,7 @@ class Config(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint32) for n in
                 ("n_layers", "n_heads", "n_kv_heads", "hidden", "ffn", "head_dim", "vocab", "max_ctx")] + \
                [("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float),
-                ("tied_lm_head", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+                ("tied_lm_head", ctypes.c_uint32), ("flags", ctypes.c_uint32)]
 
 
 class GenStats(ctypes.Structure):
@@ -81,7 +83,7 @@ SIGNATURES = {
     "frn_gguf_meta_u32": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_U32)]),
     "frn_gguf_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_U32), ctypes.POINTER(_U64),
                              ctypes.POINTER(_U32), ctypes.POINTER(_P), ctypes.POINTER(_SZ)]),
-    "frn_model_load": (_I, [_P, _I, _U32, ctypes.POINTER(_P)]),
+    "frn_model_load": (_I, [_P, _I, _U32, _U32, ctypes.POINTER(_P)]),
     "frn_generate_greedy": (_I, [_P, _P, _U32, _U32, _P, _U32, _P, ctypes.POINTER(GenStats)]),
     "frn_synth_write": (_I, [ctypes.POINTER(SynthSpec), ctypes.c_char_p]),
     "frn_quantize": (_I, [_U32, _P, _SZ, _P]),
@@ -238,7 +240,7 @@ def synth_write(path, seed, threads=0, weight_std=0.02, rope_theta=1e6, rms_eps=
 class Model:
     """A GGUF model loaded onto one GPU: Model::load + KvCache in one context."""
 
-    def __init__(self, path, device=0, max_ctx=4096):
+    def __init__(self, path, device=0, max_ctx=4096, eager=False):
         lib = load()
         self.gguf = ctypes.c_void_p()
         check(lib.frn_gguf_open(path.encode(), ctypes.byref(self.gguf)))
@@ -247,7 +249,7 @@ class Model:
         check(lib.frn_gguf_config(self.gguf, ctypes.byref(self.cfg), ctypes.byref(ctx_len)))
         self.context_length = ctx_len.value
         self.ctx = ctypes.c_void_p()
-        check(lib.frn_model_load(self.gguf, device, max_ctx, ctypes.byref(self.ctx)))
+        check(lib.frn_model_load(self.gguf, device, max_ctx, FLAG_EAGER if eager else 0, ctypes.byref(self.ctx)))
         self.cfg.max_ctx = max_ctx
         self.vocab = self.cfg.vocab
 
@@ -299,6 +301,18 @@ class Model:
                                          _ptr(stop) if stop.size else None, stop.size, _ptr(out),
                                          ctypes.byref(st)))
         return out[:st.n_generated].tolist(), st
+
+    def timings_enable(self, on=True):
+        check(load().frn_timings_enable(self.ctx, 1 if on else 0))
+
+    def timings_reset(self):
+        check(load().frn_timings_reset(self.ctx))
+
+    def timings(self):
+        arr = (Timing * 32)()
+        n = ctypes.c_uint32()
+        check(load().frn_timings(self.ctx, arr, 32, ctypes.byref(n)))
+        return {arr[i].name.decode(): (arr[i].ms, arr[i].calls) for i in range(n.value)}
 
     def close(self):
         lib = load()

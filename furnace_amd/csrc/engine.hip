@@ -11,6 +11,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
@@ -51,6 +52,14 @@ struct LayerPtrs {
 size_t type_row_bytes(uint32_t t, uint64_t in) { return (size_t)(in / blk_elems(t)) * blk_bytes(t); }
 bool known_type(uint32_t t) { return t == T_F32 || t == T_Q5_0 || t == T_Q8_0 || t == T_Q4_K || t == T_Q6_K; }
 
+// Kernel categories of the --timings dashboard.  furnace's perf.rs counters
+// (matmul, rmsnorm, rope, attn, add/swiglu, embed, sample) map onto these
+// fused kernels: rmsnorm runs in the GEMV prologues, bias/residual/SwiGLU
+// in their epilogues, the sampler's argmax in the lm_head kernel.
+enum { CAT_EMBED, CAT_QKV, CAT_ROPE, CAT_ATTN, CAT_OPROJ, CAT_GATEUP, CAT_DOWN, CAT_LMHEAD, CAT_STEP, N_CAT };
+const char* const CAT_NAMES[N_CAT] = {"embed", "qkv", "rope_kv", "attention", "o_proj", "gate_up", "down",
+                                      "lm_head", "step_end"};
+
 }  // namespace
 
 struct frn_ctx {
@@ -63,6 +72,9 @@ struct frn_ctx {
   const float* out_norm = nullptr;
   float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *act = nullptr, *logits = nullptr;
   float *part = nullptr, *kcache = nullptr, *vcache = nullptr, *rope = nullptr;
+  uint64_t* best_part = nullptr;  // per-block argmax candidates of the lm_head kernel
+  uint32_t n_best = 0;
+  uint32_t* att_count = nullptr;  // per kv head: attention splits finished (zero between launches)
   StepState* st = nullptr;
   StepState* h_st = nullptr;  // pinned mirror for read-back
   uint32_t len = 0;           // host view of KvCache::len
@@ -70,9 +82,12 @@ struct frn_ctx {
   bool finalized = false, have_logits = false;
   hipGraphExec_t g_step = nullptr, g_prefill = nullptr;
   hipGraph_t graph_step = nullptr, graph_prefill = nullptr;
+  // --timings: the step runs eagerly with an event pair around each kernel
   bool timing = false;
-  double t_ms[9] = {0};
-  uint64_t t_calls[9] = {0};
+  std::vector<hipEvent_t> ev;
+  std::vector<int> ev_cat;
+  double t_ms[N_CAT] = {0};
+  uint64_t t_calls[N_CAT] = {0};
 };
 
 static void free_ctx(frn_ctx* c) {
@@ -82,7 +97,8 @@ static void free_ctx(frn_ctx* c) {
   if (c->graph_step) (void)hipGraphDestroy(c->graph_step);
   if (c->graph_prefill) (void)hipGraphDestroy(c->graph_prefill);
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->att, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st};
+  for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->att, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part, c->att_count};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -107,7 +123,9 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
   if (c.head_dim != 64 && c.head_dim != 128) return fail(FRN_ESHAPE, "frn_create: head_dim %u unsupported (64, 128)", c.head_dim);
   if (c.n_heads / c.n_kv_heads > (c.head_dim == 64 ? 16u : 8u))
     return fail(FRN_ESHAPE, "frn_create: %u query heads per kv head unsupported", c.n_heads / c.n_kv_heads);
-  if (c.hidden % 256 || c.ffn % 32) return fail(FRN_ESHAPE, "frn_create: hidden must be a multiple of 256, ffn of 32");
+  // activation vectors are staged with 16-byte loads in 16-value chunks;
+  // per-format block divisibility is checked per tensor at upload/finalize
+  if (c.hidden % 32 || c.ffn % 32) return fail(FRN_ESHAPE, "frn_create: hidden and ffn must be multiples of 32");
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= device || device < 0)
     return fail(FRN_ENODEV, "frn_create: no HIP device %d", device);
@@ -119,6 +137,7 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
   frn_ctx* x = new frn_ctx();
   x->cfg = c;
   x->device = device;
+
   size_t kvd = (size_t)c.n_kv_heads * c.head_dim, qd = (size_t)c.n_heads * c.head_dim;
   size_t kv_bytes = (size_t)c.n_layers * c.max_ctx * kvd * 4;
   hipError_t e;
@@ -129,6 +148,8 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
       (e = dmalloc(&x->part, attention_part_floats(c.n_heads, c.head_dim, c.max_ctx) * 4)) ||
       (e = dmalloc(&x->kcache, kv_bytes)) || (e = dmalloc(&x->vcache, kv_bytes)) ||
       (e = dmalloc(&x->rope, (size_t)c.max_ctx * c.head_dim * 4)) || (e = dmalloc(&x->st, sizeof(StepState))) ||
+      (e = dmalloc(&x->best_part, ((size_t)c.vocab + 3) / 4 * 8)) ||  // >= lm_head blocks (4+ rows each)
+      (e = dmalloc(&x->att_count, (size_t)c.n_kv_heads * 4)) ||
       (e = hipHostMalloc((void**)&x->h_st, sizeof(StepState), hipHostMallocDefault))) {
     free_ctx(x);
     return hip_fail(e, "frn_create: allocation");
@@ -147,9 +168,11 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
     }
   StepState init{};
   if ((e = hipMemcpy(x->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice)) ||
+      (e = hipMemset(x->att_count, 0, (size_t)c.n_kv_heads * 4)) ||
       (e = hipMemcpy(x->st, &init, sizeof init, hipMemcpyHostToDevice)) ||
       (e = hipMemset(x->kcache, 0, kv_bytes)) || (e = hipMemset(x->vcache, 0, kv_bytes)) ||
-      (e = gemv_prepare(c.hidden > c.ffn ? c.hidden : c.ffn))) {
+      (e = gemv_prepare(std::max(gemv_lds_bytes(c.hidden, true),
+                                 std::max(gemv_lds_bytes(c.ffn, false), gemv_lds_bytes(c.n_heads * c.head_dim, false)))))) {
     free_ctx(x);
     return hip_fail(e, "frn_create: init");
   }
@@ -223,69 +246,124 @@ static frn_status need(frn_ctx* c, const std::string& name, uint64_t out, uint64
   return FRN_OK;
 }
 
-// Record one decode step on ctx->stream (under stream capture).
-static hipError_t record_step(frn_ctx* c, bool with_logits) {
+// Event pair around one kernel when the step runs eagerly for --timings.
+struct Tick {
+  frn_ctx* c;
+  bool on;
+  size_t n = 0;
+  hipError_t begin(int cat) {
+    if (!on) return hipSuccess;
+    if (c->ev.size() < 2 * (n + 1)) {
+      for (int k = 0; k < 2; ++k) {
+        hipEvent_t e;
+        hipError_t r = hipEventCreate(&e);
+        if (r) return r;
+        c->ev.push_back(e);
+      }
+      c->ev_cat.resize(c->ev.size() / 2);
+    }
+    c->ev_cat[n] = cat;
+    return hipEventRecord(c->ev[2 * n], c->stream);
+  }
+  hipError_t end(hipError_t launch) {
+    if (!on || launch) return launch;
+    hipError_t r = hipEventRecord(c->ev[2 * n + 1], c->stream);
+    ++n;
+    return r;
+  }
+};
+
+// Record one decode step on ctx->stream: under stream capture for the
+// replayed graphs, or eagerly with per-kernel events when tk.on.
+static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
   const frn_config& g = c->cfg;
   hipStream_t s = c->stream;
   hipError_t e;
   float scale = 1.0f / sqrtf((float)g.head_dim);  // model.rs:384
-  if ((e = launch_embed(c->embd->ptr, c->embd->type, g.hidden, (uint32_t)type_row_bytes(c->embd->type, g.hidden),
-                        c->st, c->x, s)))
+#define TIMED(cat, call) ((e = tk.begin(cat)) ? e : (e = tk.end(call)))
+  if (TIMED(CAT_EMBED, launch_embed(c->embd->ptr, c->embd->type, g.hidden,
+                                    (uint32_t)type_row_bytes(c->embd->type, g.hidden), c->st, c->x, s)))
     return e;
+  auto seg = [&](const DevTensor* w, const DevTensor* w2, const float* bias, float* out, const float* resid) {
+    GemvSeg sg{};
+    sg.w = w->ptr;
+    sg.w2 = w2 ? w2->ptr : nullptr;
+    sg.type = w->type;
+    sg.rows = (uint32_t)w->out;
+    sg.row_bytes = (uint32_t)type_row_bytes(w->type, w->in);
+    sg.bias = bias;
+    sg.out = out;
+    sg.resid = resid;
+    return sg;
+  };
+  auto args = [&](uint32_t in, const float* xin, const float* norm) {
+    GemvArgs a{};
+    a.in = in;
+    a.x = xin;
+    a.norm_w = norm;
+    a.eps = g.rms_eps;
+    a.n_seg = 1;
+    return a;
+  };
+  const uint32_t H = g.hidden, QD = g.n_heads * g.head_dim;
   for (uint32_t l = 0; l < g.n_layers; ++l) {
     const LayerPtrs& L = c->layers[l];
-    auto gemv = [&](const DevTensor* w, const DevTensor* w2, const float* xin, const float* norm, const float* bias,
-                    float* out, GemvMode mode) {
-      GemvArgs a{};
-      a.w = w->ptr;
-      a.w2 = w2 ? w2->ptr : nullptr;
-      a.type = w->type;
-      a.rows = (uint32_t)w->out;
-      a.in = (uint32_t)w->in;
-      a.row_bytes = (uint32_t)type_row_bytes(w->type, w->in);
-      a.x = xin;
-      a.norm_w = norm;
-      a.eps = g.rms_eps;
-      a.bias = bias;
-      a.out = out;
-      a.state = c->st;
-      return launch_gemv(a, mode, s);
-    };
-    if ((e = gemv(L.wq, nullptr, c->x, L.attn_norm, L.bq, c->q, GEMV_STORE)) ||
-        (e = gemv(L.wk, nullptr, c->x, L.attn_norm, L.bk, c->k, GEMV_STORE)) ||
-        (e = gemv(L.wv, nullptr, c->x, L.attn_norm, L.bv, c->v, GEMV_STORE)))
-      return e;
+    // rmsnorm + q/k/v GEMVs + biases in one launch (model.rs:456-459)
+    GemvArgs qkv = args(H, c->x, L.attn_norm);
+    qkv.n_seg = 3;
+    qkv.seg[0] = seg(L.wq, nullptr, L.bq, c->q, nullptr);
+    qkv.seg[1] = seg(L.wk, nullptr, L.bk, c->k, nullptr);
+    qkv.seg[2] = seg(L.wv, nullptr, L.bv, c->v, nullptr);
+    if (TIMED(CAT_QKV, launch_gemv(qkv, GEMV_STORE, s))) return e;
+    // rope, KV append, attention (model.rs:460-467)
     size_t lo = (size_t)l * g.max_ctx * g.n_kv_heads * g.head_dim;
-    if ((e = launch_rope_kv(c->q, c->k, c->v, c->rope, g.n_heads, g.n_kv_heads, g.head_dim, c->kcache + lo,
-                            c->vcache + lo, c->st, s)))
+    if (TIMED(CAT_ATTN, launch_attention(c->q, c->k, c->v, c->rope, c->kcache + lo, c->vcache + lo, g.n_heads,
+                                         g.n_kv_heads, g.head_dim, g.max_ctx, scale, c->part, c->att_count, c->att,
+                                         c->st, s)))
       return e;
-    if ((e = launch_attention(c->q, c->kcache + lo, c->vcache + lo, g.n_heads, g.n_kv_heads, g.head_dim, g.max_ctx,
-                              scale, c->part, c->att, c->st, s)))
-      return e;
-    if ((e = gemv(L.wo, nullptr, c->att, nullptr, nullptr, c->x, GEMV_RESID))) return e;
-    if ((e = gemv(L.gate, L.up, c->x, L.ffn_norm, nullptr, c->act, GEMV_SWIGLU))) return e;
-    if ((e = gemv(L.down, nullptr, c->act, nullptr, nullptr, c->x, GEMV_RESID))) return e;
+    // o-proj + residual (model.rs:469-470)
+    GemvArgs o = args(QD, c->att, nullptr);
+    o.seg[0] = seg(L.wo, nullptr, nullptr, c->x, c->x);
+    if (TIMED(CAT_OPROJ, launch_gemv(o, GEMV_RESID, s))) return e;
+    // rmsnorm + gate/up + SwiGLU (model.rs:473-476)
+    GemvArgs gu = args(H, c->x, L.ffn_norm);
+    gu.seg[0] = seg(L.gate, L.up, nullptr, c->act, nullptr);
+    if (TIMED(CAT_GATEUP, launch_gemv(gu, GEMV_SWIGLU, s))) return e;
+    // down + residual (model.rs:476-477)
+    GemvArgs dn = args(g.ffn, c->act, nullptr);
+    dn.seg[0] = seg(L.down, nullptr, nullptr, c->x, c->x);
+    if (TIMED(CAT_DOWN, launch_gemv(dn, GEMV_RESID, s))) return e;
   }
-  if (with_logits) {
-    GemvArgs a{};
-    a.w = c->lm_head->ptr;
-    a.type = c->lm_head->type;
-    a.rows = g.vocab;
-    a.in = g.hidden;
-    a.row_bytes = (uint32_t)type_row_bytes(a.type, g.hidden);
-    a.x = c->x;
-    a.norm_w = c->out_norm;
-    a.eps = g.rms_eps;
-    a.out = c->logits;
-    a.state = c->st;
-    if ((e = launch_gemv(a, GEMV_ARGMAX, s))) return e;
+  if (with_logits) {  // last_row_logits + argmax (model.rs:594-600, generate.rs:69-77)
+    GemvArgs lm = args(H, c->x, c->out_norm);
+    lm.seg[0] = seg(c->lm_head, nullptr, nullptr, c->logits, nullptr);
+    lm.best = c->best_part;
+    if (TIMED(CAT_LMHEAD, launch_gemv(lm, GEMV_ARGMAX, s, &c->n_best))) return e;
   }
-  return launch_step_end(c->st, with_logits ? 1 : 0, s);
+  TIMED(CAT_STEP, launch_step_end(c->st, with_logits ? c->best_part : nullptr, c->n_best, s));
+#undef TIMED
+  return e;
+}
+
+// Eager step with per-kernel events, accumulated into the dashboard.
+static hipError_t timed_step(frn_ctx* c, bool with_logits) {
+  Tick tk{c, true};
+  hipError_t e = record_step(c, with_logits, tk);
+  if (e) return e;
+  if ((e = hipEventSynchronize(c->ev[2 * tk.n - 1]))) return e;
+  for (size_t i = 0; i < tk.n; ++i) {
+    float ms = 0.f;
+    if ((e = hipEventElapsedTime(&ms, c->ev[2 * i], c->ev[2 * i + 1]))) return e;
+    c->t_ms[c->ev_cat[i]] += ms;
+    c->t_calls[c->ev_cat[i]] += 1;
+  }
+  return hipSuccess;
 }
 
 static frn_status capture(frn_ctx* c, bool with_logits, hipGraph_t* graph, hipGraphExec_t* exec) {
   HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-  hipError_t e = record_step(c, with_logits);
+  Tick tk{c, false};
+  hipError_t e = record_step(c, with_logits, tk);
   hipGraph_t gr = nullptr;
   hipError_t e2 = hipStreamEndCapture(c->stream, &gr);
   if (e) {
@@ -340,8 +418,10 @@ extern "C" frn_status frn_finalize(frn_ctx* c) {
       return fail(FRN_EDTYPE, "blk.%u: ffn_gate and ffn_up must share a type for the fused SwiGLU kernel", l);
   }
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
-  if ((st = capture(c, true, &c->graph_step, &c->g_step))) return st;
-  if ((st = capture(c, false, &c->graph_prefill, &c->g_prefill))) return st;
+  if (!(g.flags & FRN_FLAG_EAGER)) {
+    if ((st = capture(c, true, &c->graph_step, &c->g_step))) return st;
+    if ((st = capture(c, false, &c->graph_prefill, &c->g_prefill))) return st;
+  }
   c->finalized = true;
   return FRN_OK;
 }
@@ -354,7 +434,14 @@ static frn_status run_step(frn_ctx* c, uint32_t tok, bool with_logits) {
     HIP_TRY(hipMemcpyAsync((char*)c->st + offsetof(StepState, tok), &c->h_st->tok, 4, hipMemcpyHostToDevice, c->stream),
             "token upload");
   }
-  HIP_TRY(hipGraphLaunch(with_logits ? c->g_step : c->g_prefill, c->stream), "hipGraphLaunch");
+  if (c->timing) {
+    HIP_TRY(timed_step(c, with_logits), "timed step");
+  } else if (c->cfg.flags & FRN_FLAG_EAGER) {
+    Tick tk{c, false};
+    HIP_TRY(record_step(c, with_logits, tk), "eager step");
+  } else {
+    HIP_TRY(hipGraphLaunch(with_logits ? c->g_step : c->g_prefill, c->stream), "hipGraphLaunch");
+  }
   c->len += 1;
   c->last_next = 0xFFFFFFFFu;
   return FRN_OK;
@@ -458,11 +545,10 @@ extern "C" frn_status frn_timings_reset(frn_ctx* c) {
   return FRN_OK;
 }
 extern "C" frn_status frn_timings(frn_ctx* c, frn_timing* out, uint32_t max, uint32_t* n) {
-  static const char* names[9] = {"matmul", "rmsnorm", "softmax", "rope", "attn scores", "attn apply", "add/swiglu", "embed", "sample"};
-  if (!c || !n) return fail(FRN_EINVAL, "null argument");
+  if (!c || !n || (max && !out)) return fail(FRN_EINVAL, "null argument");
   uint32_t k = 0;
-  for (int i = 0; i < 9 && k < max; ++i) {
-    snprintf(out[k].name, sizeof out[k].name, "%s", names[i]);
+  for (int i = 0; i < N_CAT && k < max; ++i) {
+    snprintf(out[k].name, sizeof out[k].name, "%s", CAT_NAMES[i]);
     out[k].ms = c->t_ms[i];
     out[k].calls = c->t_calls[i];
     ++k;
@@ -497,23 +583,24 @@ extern "C" frn_status frn_matmul_quant(uint32_t type, const void* w_dev, size_t 
   // the kernels use 16-byte loads of rows and of the activation vector
   if (((uintptr_t)w_dev | (uintptr_t)a_dev) & 15)
     return fail(FRN_EINVAL, "frn_matmul_quant: w_dev and a_dev must be 16-byte aligned");
-  if (gemv_lds_bytes(type, d_in) > 160 * 1024)
+  if (gemv_lds_bytes(d_in, false) > 160 * 1024)
     return fail(FRN_ESHAPE, "matmul: in dim %u exceeds the 160 KiB LDS staging limit", d_in);
-  if (seq == 0 || d_out == 0) return FRN_OK;
-  static uint32_t prepared = 0;
-  if (d_in > prepared) {
-    HIP_TRY(gemv_prepare(d_in), "gemv_prepare");
-    prepared = d_in;
+  static size_t prepared = 0;
+  if (gemv_lds_bytes(d_in, false) > prepared) {
+    HIP_TRY(gemv_prepare(gemv_lds_bytes(d_in, false)), "gemv_prepare");
+    prepared = gemv_lds_bytes(d_in, false);
   }
+  if (seq == 0 || d_out == 0) return FRN_OK;
   for (uint32_t s = 0; s < seq; ++s) {
     GemvArgs a{};
-    a.w = (const uint8_t*)w_dev;
-    a.type = type;
-    a.rows = d_out;
+    a.n_seg = 1;
     a.in = d_in;
-    a.row_bytes = (uint32_t)type_row_bytes(type, d_in);
     a.x = a_dev + (size_t)s * d_in;
-    a.out = out_dev + (size_t)s * d_out;
+    a.seg[0].w = (const uint8_t*)w_dev;
+    a.seg[0].type = type;
+    a.seg[0].rows = d_out;
+    a.seg[0].row_bytes = (uint32_t)type_row_bytes(type, d_in);
+    a.seg[0].out = out_dev + (size_t)s * d_out;
     HIP_TRY(launch_gemv(a, GEMV_STORE, (hipStream_t)stream), "gemv launch");
   }
   return FRN_OK;

@@ -43,13 +43,14 @@ static int cmd_run(int argc, char** argv) {
   std::vector<uint32_t> ids;
   uint32_t max_new = 50, max_ctx = 0;
   int device = 0;
-  bool timings = false;
+  bool timings = false, eager = false;
   for (int i = 1; i < argc; ++i) {
     if (!strcmp(argv[i], "--prompt-ids") && i + 1 < argc) ids = parse_ids(argv[++i]);
     else if ((!strcmp(argv[i], "-n") || !strcmp(argv[i], "--max-tokens")) && i + 1 < argc) max_new = (uint32_t)atoi(argv[++i]);
     else if (!strcmp(argv[i], "--max-ctx") && i + 1 < argc) max_ctx = (uint32_t)atoi(argv[++i]);
     else if (!strcmp(argv[i], "--device") && i + 1 < argc) device = atoi(argv[++i]);
     else if (!strcmp(argv[i], "--timings")) timings = true;
+    else if (!strcmp(argv[i], "--eager")) eager = true;
     else if (!strcmp(argv[i], "--temp") && i + 1 < argc) {
       if (atof(argv[++i]) != 0.0) return fprintf(stderr, "Error: only --temp 0 (greedy) runs on the GPU path\n"), 2;
     } else return fprintf(stderr, "Error: unknown argument %s\n", argv[i]), 2;
@@ -69,7 +70,7 @@ static int cmd_run(int argc, char** argv) {
     return 1;
   }
   frn_ctx* ctx;
-  if (frn_model_load(g, device, max_ctx, &ctx)) return die("load");
+  if (frn_model_load(g, device, max_ctx, eager ? FRN_FLAG_EAGER : 0, &ctx)) return die("load");
   fprintf(stderr, "weights: uploaded raw to HBM in %.2f s\n", now_s() - t0);
   fprintf(stderr, "prompt: %zu tokens\n", ids.size());
   uint32_t stop[2];

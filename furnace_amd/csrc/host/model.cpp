@@ -86,13 +86,15 @@ extern "C" frn_status frn_gguf_config(const frn_gguf* g, frn_config* c, uint32_t
   return FRN_OK;
 }
 
-extern "C" frn_status frn_model_load(const frn_gguf* g, int device, uint32_t max_ctx, frn_ctx** out) {
+extern "C" frn_status frn_model_load(const frn_gguf* g, int device, uint32_t max_ctx, uint32_t flags,
+                                     frn_ctx** out) {
   if (!g || !out) return frn_fail(FRN_EINVAL, "frn_model_load: null argument");
   *out = nullptr;
   frn_config c{};
   frn_status st = frn_gguf_config(g, &c, nullptr);
   if (st) return st;
   c.max_ctx = max_ctx;
+  c.flags = flags;
   frn_ctx* ctx = nullptr;
   if ((st = frn_create(&c, device, &ctx))) return st;
   // every tensor of the file goes up raw; finalize checks that the set

@@ -12,40 +12,56 @@ namespace frn {
 struct StepState {
   uint32_t pos;        // position of the token being processed (KvCache::len)
   uint32_t tok;        // its id
-  uint64_t best;       // packed (ordered logit, ~index) running argmax
   uint32_t next_tok;   // argmax of this step's logits
-  uint32_t pad[3];
+  uint32_t pad[5];
 };
 
 enum GemvMode : int { GEMV_STORE = 0, GEMV_RESID = 1, GEMV_SWIGLU = 2, GEMV_ARGMAX = 3 };
 
+// One weight matrix of a (possibly multi-matrix) GEMV launch.  All segments
+// of a launch share the input vector x and its optional rmsnorm.
+struct GemvSeg {
+  const uint8_t* w;   // [rows, row_bytes] raw blocks
+  const uint8_t* w2;  // SWIGLU: the up matrix (w is gate)
+  uint32_t type, rows, row_bytes, block0;  // block0: first block of this segment
+  const float* bias;  // optional [rows]
+  float* out;         // [rows]; RESID: out[r] = resid[r] + dot
+  const float* resid; // RESID: residual input (may equal out)
+  float* out2;        // RESID: optional second copy of the result
+};
+
 struct GemvArgs {
-  const uint8_t* w;      // [rows, row_bytes] raw blocks
-  const uint8_t* w2;     // SWIGLU: the up matrix (w is gate)
-  uint32_t type, rows, in, row_bytes;
-  const float* x;        // [in]
-  const float* norm_w;   // optional rmsnorm gain applied to x first
+  GemvSeg seg[3];
+  int n_seg;
+  uint32_t in;
+  const float* x;       // [in]
+  const float* norm_w;  // optional rmsnorm gain applied to x first (tensor.rs:164-185)
   float eps;
-  const float* bias;     // optional [rows]
-  float* out;            // [rows]; RESID: out[r] += dot (in place)
-  StepState* state;      // ARGMAX: running argmax target
+  uint64_t* best;       // ARGMAX: one packed (logit, ~row) candidate per block
 };
 
 hipError_t launch_dequant(uint32_t type, const uint8_t* raw, size_t n_elems, float* out, hipStream_t s);
-hipError_t launch_gemv(const GemvArgs& a, GemvMode mode, hipStream_t s);
-size_t gemv_lds_bytes(uint32_t type, uint32_t in);
-hipError_t gemv_prepare(uint32_t max_in);  // raises dynamic-LDS limits once
+// Launches one GEMV over args.n_seg segments (mode applies to all).
+// Returns the number of blocks launched through *blocks when non-null.
+hipError_t launch_gemv(GemvArgs a, GemvMode mode, hipStream_t s, uint32_t* blocks = nullptr);
+size_t gemv_lds_bytes(uint32_t in, bool norm);
+hipError_t gemv_prepare(size_t max_lds_bytes);  // raises dynamic-LDS limits once
+// Blocks launch_gemv uses for a single segment of `rows` rows and in `in`.
+uint32_t gemv_blocks(uint32_t type, uint32_t rows, uint32_t in);
 
 hipError_t launch_embed(const uint8_t* table, uint32_t type, uint32_t hidden, uint32_t row_bytes, StepState* st,
                         float* x, hipStream_t s);
-hipError_t launch_rope_kv(float* q, const float* k, const float* v, const float* rope_cs, uint32_t n_heads,
-                          uint32_t n_kv_heads, uint32_t head_dim, float* k_cache, float* v_cache, const StepState* st,
-                          hipStream_t s);
-hipError_t launch_attention(const float* q, const float* k_cache, const float* v_cache, uint32_t n_heads,
-                            uint32_t n_kv_heads, uint32_t head_dim, uint32_t max_ctx, float scale, float* part,
-                            float* att, const StepState* st, hipStream_t s);
+// RoPE(q), RoPE(k) at the step's position, KV-cache append, split-sequence
+// GQA attention and the split combine, in one launch.  counters holds
+// n_kv_heads zeroed words (left zeroed on exit).
+hipError_t launch_attention(const float* q, const float* k, const float* v, const float* rope_cs, float* k_cache,
+                            float* v_cache, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                            uint32_t max_ctx, float scale, float* part, uint32_t* counters, float* att,
+                            const StepState* st, hipStream_t s);
 size_t attention_part_floats(uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx);
-hipError_t launch_step_end(StepState* st, int has_logits, hipStream_t s);
+// Ends a step: reduces the lm_head kernel's per-block argmax candidates
+// (best == nullptr for a step without logits) and advances the position.
+hipError_t launch_step_end(StepState* st, const uint64_t* best, uint32_t n_best, hipStream_t s);
 hipError_t launch_argmax(const float* x, size_t n, uint64_t* scratch, uint32_t* out, hipStream_t s);
 
 }  // namespace frn

@@ -50,8 +50,12 @@ typedef struct frn_config {
   uint32_t n_layers, n_heads, n_kv_heads, hidden, ffn, head_dim, vocab, max_ctx;
   float rope_theta, rms_eps;
   uint32_t tied_lm_head; /* 1 when output.weight is absent (model.rs:541-545) */
-  uint32_t reserved;
+  uint32_t flags;        /* FRN_FLAG_* */
 } frn_config;
+
+/* Launch the step's kernels one by one instead of replaying a hipGraph
+ * (same kernels; for profilers that do not follow graph launches). */
+#define FRN_FLAG_EAGER 1u
 
 typedef struct frn_ctx frn_ctx;
 
@@ -102,12 +106,12 @@ void frn_destroy(frn_ctx* ctx);
 /* Message for the last failure on this thread ("" if none). */
 const char* frn_last_error(void);
 
-/* --timings dashboard (perf.rs:25-96): per-category GPU time of the decode
- * steps since the last frn_timings_reset, measured with HIP events around
- * each kernel when enabled.  Categories follow perf.rs's counters
- * (matmul, rmsnorm, softmax, rope, attn scores, attn apply, add/swiglu,
- * embed, sample); kernels that fuse several ops report under the op that
- * dominates their bytes. */
+/* --timings dashboard (perf.rs:25-96): per-kernel GPU time of the steps run
+ * since the last frn_timings_reset.  While enabled, steps run eagerly (not
+ * as a graph) with a HIP event pair around every kernel.  Entries: embed,
+ * qkv, rope_kv, attention, o_proj, gate_up, down, lm_head, step_end.
+ * perf.rs's matmul counter is qkv + o_proj + gate_up + down + lm_head; its
+ * rmsnorm, add/swiglu and sample work is fused into those kernels. */
 typedef struct frn_timing {
   char name[16];
   double ms;

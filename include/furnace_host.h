@@ -31,8 +31,9 @@ frn_status frn_gguf_tensor(const frn_gguf* g, const char* name, uint32_t* type, 
                            const void** data, size_t* bytes);
 
 /* Model::load (model.rs:520-552) onto HIP device `device`: Config from the
- * metadata, one frn_upload per tensor of the model, frn_finalize. */
-frn_status frn_model_load(const frn_gguf* g, int device, uint32_t max_ctx, frn_ctx** out);
+ * metadata, one frn_upload per tensor of the model, frn_finalize.  flags are
+ * FRN_FLAG_* of furnace_hip.h. */
+frn_status frn_model_load(const frn_gguf* g, int device, uint32_t max_ctx, uint32_t flags, frn_ctx** out);
 
 typedef struct frn_gen_stats {
   double prefill_s;      /* generate.rs:109-111 */

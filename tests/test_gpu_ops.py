@@ -72,6 +72,8 @@ def _gemv_case(hip, gtype, d_out, d_in, seed, seq=1):
     got = hip.from_device(d_y, (seq, d_out), np.float32)
     for p in (d_w, d_x, d_y):
         hip.free(p)
+    if gtype == fa.F32:  # F32 weights take tensor::matmul (tensor.rs:74-80)
+        return got, orc.matmul_f32(x, raw.view(np.float32).reshape(d_out, d_in))
     return got, orc.matmul_quant(x, raw, d_out, d_in, gtype)
 
 
