@@ -15,8 +15,8 @@
 // row whose bytes it loads with 16-byte (or dword-aligned) loads, so that a
 // group of lanes reads one contiguous stretch of the row.  Q4_K superblocks
 // (144 B) keep 16-byte alignment; Q6_K (210 B), Q8_0 (34 B) and Q5_0 (22 B)
-// blocks only keep 2-byte alignment, which load16_at() repairs with
-// v_alignbyte_b32 without reading outside the block.
+// blocks only keep 2-byte alignment, which the items repair in registers
+// with v_alignbyte_b32, never reading outside the block.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -36,23 +36,6 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
 }
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *(const uint16_t*)p; }
-__device__ __forceinline__ uint32_t ld_u8(const uint8_t* p) { return *p; }
-
-// 16 bytes starting at a 2-byte aligned address p, realigned in registers.
-// Reads only [p & ~3, p + 18) when p % 4 == 2 and [p, p + 16) otherwise, so
-// it never touches bytes outside the 2 bytes before and after the field.
-__device__ __forceinline__ uint4 load16_at(const uint8_t* p) {
-  uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
-  const uint32_t* base = (const uint32_t*)(p - sh);  // pointer arithmetic keeps the global address space
-  uint32_t w0 = base[0], w1 = base[1], w2 = base[2], w3 = base[3];
-  uint32_t w4 = base[sh ? 4 : 3];
-  uint4 r;
-  r.x = __builtin_amdgcn_alignbyte(w1, w0, sh);
-  r.y = __builtin_amdgcn_alignbyte(w2, w1, sh);
-  r.z = __builtin_amdgcn_alignbyte(w3, w2, sh);
-  r.w = __builtin_amdgcn_alignbyte(w4, w3, sh);
-  return r;
-}
 
 // Byte k of w as float; the backend selects v_cvt_f32_ubyte{k}.
 __device__ __forceinline__ float byte_f(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }
@@ -71,17 +54,16 @@ __device__ __forceinline__ void q4k_scale_min(int j, const uint8_t* s, uint32_t&
 }
 
 // q4k_scale_min on the 12 scale bytes held as three dwords s0..3 | s4..7 |
-// s8..11 (no byte addressing of registers).
+// s8..11 (no byte addressing of registers).  Both forms are computed and
+// selected, so a lane-dependent j costs no branch.
 __device__ __forceinline__ void q4k_scale_min_regs(uint32_t a, uint32_t b, uint32_t c, int j, uint32_t& sc,
                                                    uint32_t& m) {
-  if (j < 4) {
-    sc = (a >> (8 * j)) & 63u;
-    m = (b >> (8 * j)) & 63u;
-  } else {
-    int jj = 8 * (j - 4);
-    sc = ((c >> jj) & 0x0Fu) | (((a >> (jj + 6)) & 3u) << 4);
-    m = ((c >> (jj + 4)) & 0x0Fu) | (((b >> (jj + 6)) & 3u) << 4);
-  }
+  const uint32_t lo = 8u * (j & 3);
+  const uint32_t sc_lo = (a >> lo) & 63u, m_lo = (b >> lo) & 63u;
+  const uint32_t sc_hi = ((c >> lo) & 0x0Fu) | (((a >> (lo + 6)) & 3u) << 4);
+  const uint32_t m_hi = ((c >> (lo + 4)) & 0x0Fu) | (((b >> (lo + 6)) & 3u) << 4);
+  sc = j < 4 ? sc_lo : sc_hi;
+  m = j < 4 ? m_lo : m_hi;
 }
 
 // Value i of one block (quant.rs:17-42, 53-63, 93-109, 114-133).
@@ -176,24 +158,62 @@ __device__ __forceinline__ float qx16_wide(const uint32_t* q, const XLds& X, uin
 
 // ---- GEMV items ---------------------------------------------------------
 // Each item is split into load() -- the raw bytes of one 32- or 64-value
-// slice of a weight row, fetched into registers -- and dot() -- decode and
-// multiply with the staged activation vector -- so a lane can issue the
-// loads of several items before waiting on any of them.
+// slice of a weight row, fetched with raw buffer loads -- and dot() --
+// realign, decode and multiply with the staged activation vector.  Loads
+// go through a buffer resource whose range is the weight matrix: an item
+// of a row past the end, or past the row's last block, is given an offset
+// >= BUF_INVALID, which the hardware range check turns into zeros without
+// a memory access.  So every lane issues the same load sequence with no
+// branches, and the compiler can keep a whole batch in flight (a predicated
+// load, or one whose data is realigned right away, makes it wait on the
+// spot).  All zero bytes decode to zero weights (every scale is zero), and
+// the chunk index of such an item is clamped, so its dot is exactly 0.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr uint32_t BUF_INVALID = 0x80000000u;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  // dword3 0x00020000: raw (untyped, unswizzled) 32-bit data format on gfx9
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bl128(rsrc_t r, uint32_t off) {
+  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 bl64(rsrc_t r, uint32_t off) {
+  u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t bl32(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bl16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+// 16 bytes at a 2-byte aligned offset, from the 20 bytes loaded at the
+// dword below it: w = dwords [off & ~3, +16), x = the dword after.
+__device__ __forceinline__ void realign16(const uint4& w, uint32_t x, uint32_t sh, uint32_t (&o)[4]) {
+  o[0] = __builtin_amdgcn_alignbyte(w.y, w.x, sh);
+  o[1] = __builtin_amdgcn_alignbyte(w.z, w.y, sh);
+  o[2] = __builtin_amdgcn_alignbyte(w.w, w.z, sh);
+  o[3] = __builtin_amdgcn_alignbyte(x, w.w, sh);
+}
 
 // Q4_K: 8 items per superblock.  Item (k, j), j = 2*j64 + hh, covers the 16
 // quant bytes qs[32*j64 + 16*hh .. +16]: low nibbles are values
 // 64*j64 + 16*hh + [0,16) of sub-block 2*j64, high nibbles values
 // 64*j64 + 32 + 16*hh + [0,16) of sub-block 2*j64+1.  Factorised as
-// (d*sc)*sum(q*x) - (dmin*m)*sum(x).
+// (d*sc)*sum(q*x) - (dmin*m)*sum(x).  Superblocks are 16-byte aligned.
 struct Q4KRaw {
   uint4 hdr, q;
 };
-__device__ __forceinline__ Q4KRaw q4k_load(const uint8_t* row, int item) {
-  const uint8_t* sb = row + (size_t)(item >> 3) * 144;
-  Q4KRaw r;
-  r.hdr = *(const uint4*)sb;
-  r.q = *(const uint4*)(sb + 16 + 16 * (item & 7));
-  return r;
+__device__ __forceinline__ Q4KRaw q4k_load(rsrc_t r, uint32_t row, int item) {
+  const uint32_t sb = row + (uint32_t)(item >> 3) * 144u;
+  Q4KRaw o;
+  o.hdr = bl128(r, sb);
+  o.q = bl128(r, sb + 16u + 16u * (item & 7));
+  return o;
 }
 __device__ __forceinline__ float q4k_dot(const Q4KRaw& r, int item, const XLds& X) {
   int k = item >> 3, j = item & 7, j64 = j >> 1, hh = j & 1;
@@ -214,27 +234,38 @@ __device__ __forceinline__ float q4k_dot(const Q4KRaw& r, int item, const XLds& 
 // l = 16*lq + [0,16), quarter pair p selects k6 in {p, p+2}:
 //   k6 = p   -> low nibbles of ql[64h + 32p + l]  with qh bits 2p..2p+1
 //   k6 = p+2 -> high nibbles of the same bytes     with qh bits 2p+4..2p+5
-// values 128h + 32*k6 + l, sub-scales sc[8h + 2*k6 + lq].
+// values 128h + 32*k6 + l, sub-scales sc[8h + 2*k6 + lq].  Superblocks
+// (210 B) are only 2-byte aligned: ql and qh come as 20 bytes from the
+// dword below and are realigned in dot(); the two scale bytes (4 apart)
+// come in one 8-byte load from the dword below the first; d by itself.
 struct Q6KRaw {
   uint4 ql, qh;
-  uint32_t d, s0, s1;
+  uint32_t qlx, qhx;
+  uint2 sc;
+  uint32_t d;
 };
-__device__ __forceinline__ Q6KRaw q6k_load(const uint8_t* row, int item) {
-  int k = item >> 3, r = item & 7, h = r >> 2, lq = (r >> 1) & 1, p = r & 1;
-  const uint8_t* sb = row + (size_t)k * 210;
+__device__ __forceinline__ Q6KRaw q6k_load(rsrc_t r, uint32_t row, int item) {
+  int k = item >> 3, rr = item & 7, h = rr >> 2, lq = (rr >> 1) & 1, p = rr & 1;
+  const uint32_t sb = row + (uint32_t)k * 210u;
+  const uint32_t a = (sb + 64u * h + 32u * p + 16u * lq) & ~3u, b = (sb + 128u + 32u * h + 16u * lq) & ~3u;
   Q6KRaw o;
-  o.ql = load16_at(sb + 64 * h + 32 * p + 16 * lq);
-  o.qh = load16_at(sb + 128 + 32 * h + 16 * lq);
-  o.d = ld_u16(sb + 208);
-  o.s0 = ld_u8(sb + 192 + 8 * h + 2 * p + lq);
-  o.s1 = ld_u8(sb + 192 + 8 * h + 2 * (p + 2) + lq);
+  o.ql = bl128(r, a);
+  o.qlx = bl32(r, a + 16u);
+  o.qh = bl128(r, b);
+  o.qhx = bl32(r, b + 16u);
+  o.sc = bl64(r, (sb + 192u + 8u * h + 2u * p + lq) & ~3u);
+  o.d = bl16(r, sb + 208u);
   return o;
 }
-__device__ __forceinline__ float q6k_dot(const Q6KRaw& o, int item, const XLds& X) {
-  int k = item >> 3, r = item & 7, h = r >> 2, lq = (r >> 1) & 1, p = r & 1;
-  float d = f16_bits_to_f32(o.d);
-  float s0 = (float)(int8_t)o.s0, s1 = (float)(int8_t)o.s1;
-  uint32_t lw[4] = {o.ql.x, o.ql.y, o.ql.z, o.ql.w}, hw[4] = {o.qh.x, o.qh.y, o.qh.z, o.qh.w};
+__device__ __forceinline__ float q6k_dot(const Q6KRaw& o, uint32_t row, int item, const XLds& X) {
+  int k = item >> 3, rr = item & 7, h = rr >> 2, lq = (rr >> 1) & 1, p = rr & 1;
+  const uint32_t sb = row + (uint32_t)k * 210u, sh = sb & 3u;
+  const uint32_t ss = 8u * ((sb + 192u + 8u * h + 2u * p + lq) & 3u);
+  float d = f16_bits_to_f32(o.d & 0xFFFFu);
+  float s0 = (float)(int8_t)((o.sc.x >> ss) & 0xFFu), s1 = (float)(int8_t)((o.sc.y >> ss) & 0xFFu);
+  uint32_t lw[4], hw[4];
+  realign16(o.ql, o.qlx, sh, lw);
+  realign16(o.qh, o.qhx, sh, hw);
   uint32_t v0[4], v1[4];
   const uint32_t sh0 = 2 * p, sh1 = 2 * p + 4;
 #pragma unroll
@@ -249,17 +280,22 @@ __device__ __forceinline__ float q6k_dot(const Q6KRaw& o, int item, const XLds& 
 // Q8_0, rows with an even number of blocks: item = block pair (68 B,
 // dword aligned): d0 | 32 q | d1 | 32 q.
 struct Q8PairRaw {
-  uint32_t v[17];
+  uint4 a, b, c, e;
+  uint32_t f;
 };
-__device__ __forceinline__ Q8PairRaw q8_0_pair_load(const uint8_t* row, int item) {
-  const uint32_t* w = (const uint32_t*)(row + (size_t)item * 68);
-  Q8PairRaw r;
-#pragma unroll
-  for (int i = 0; i < 17; ++i) r.v[i] = w[i];
-  return r;
+__device__ __forceinline__ Q8PairRaw q8_0_pair_load(rsrc_t r, uint32_t row, int item) {
+  const uint32_t o = row + 68u * (uint32_t)item;
+  Q8PairRaw v;
+  v.a = bl128(r, o);
+  v.b = bl128(r, o + 16u);
+  v.c = bl128(r, o + 32u);
+  v.e = bl128(r, o + 48u);
+  v.f = bl32(r, o + 64u);
+  return v;
 }
 __device__ __forceinline__ float q8_0_pair_dot(const Q8PairRaw& r, int item, const XLds& X) {
-  const uint32_t* v = r.v;
+  const uint32_t v[17] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c.x,
+                          r.c.y, r.c.z, r.c.w, r.e.x, r.e.y, r.e.z, r.e.w, r.f};
   float d0 = f16_bits_to_f32(v[0] & 0xFFFFu), d1 = f16_bits_to_f32(v[8] >> 16);
   uint32_t q0[8];
 #pragma unroll
@@ -273,17 +309,21 @@ __device__ __forceinline__ float q8_0_pair_dot(const Q8PairRaw& r, int item, con
 // Q5_0, rows with an even number of blocks: item = block pair (44 B), on
 // the f32 vector.
 struct Q5PairRaw {
-  uint32_t v[11];
+  uint4 a, b;
+  uint2 c;
+  uint32_t e;
 };
-__device__ __forceinline__ Q5PairRaw q5_0_pair_load(const uint8_t* row, int item) {
-  const uint32_t* w = (const uint32_t*)(row + (size_t)item * 44);
-  Q5PairRaw r;
-#pragma unroll
-  for (int i = 0; i < 11; ++i) r.v[i] = w[i];
-  return r;
+__device__ __forceinline__ Q5PairRaw q5_0_pair_load(rsrc_t r, uint32_t row, int item) {
+  const uint32_t o = row + 44u * (uint32_t)item;
+  Q5PairRaw v;
+  v.a = bl128(r, o);
+  v.b = bl128(r, o + 16u);
+  v.c = bl64(r, o + 32u);
+  v.e = bl32(r, o + 40u);
+  return v;
 }
 __device__ __forceinline__ float q5_0_pair_dot(const Q5PairRaw& r, int item, const float* xs) {
-  const uint32_t* v = r.v;
+  const uint32_t v[11] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c.x, r.c.y, r.e};
   // block 0: d0 = bytes 0..2, qh0 = bytes 2..6, qs0 = bytes 6..22
   // block 1: d1 = bytes 22..24, qh1 = bytes 24..28, qs1 = bytes 28..44
   float d0 = f16_bits_to_f32(v[0] & 0xFFFFu), d1 = f16_bits_to_f32(v[5] >> 16);
@@ -310,7 +350,8 @@ __device__ __forceinline__ float q5_0_pair_dot(const Q5PairRaw& r, int item, con
 }
 
 // Odd block counts (Q8_0/Q5_0 rows of 32*odd values): one block per item,
-// byte loads.  Correct for any 2-byte alignment; only used off the hot path.
+// byte loads from the row pointer at dot time.  Correct for any 2-byte
+// alignment; only used off the hot path.
 __device__ __forceinline__ float small_block_item(uint32_t t, const uint8_t* row, int item, const float* xs) {
   const uint8_t* b = row + (size_t)item * blk_bytes(t);
   float d = f16_bits_to_f32(ld_u16(b));

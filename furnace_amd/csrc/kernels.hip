@@ -58,169 +58,184 @@ __host__ __device__ inline int items_per_row(uint32_t t, uint32_t in, bool pairs
   return (int)(in / 16);  // F32: 16 floats per item
 }
 
-// Per-format raw-register type and prefetch depth (items in flight per lane).
+// Items of one row a lane loads per pipeline step: 3 for the K-quants, 2
+// for the others, one less for SWIGLU (two rows per lane) to stay within
+// the registers of 2 blocks per CU.
+__host__ __device__ constexpr int gemv_bi(uint32_t t, int mode) {
+  return (t == T_Q4_K || t == T_Q6_K ? 3 : 2) - (mode == GEMV_SWIGLU ? 1 : 0);
+}
+
+// Per-format raw-register type.  dot() gets the row's byte offset (alignment of the
+// 2-byte aligned formats) and its pointer (nullptr for a masked item; only
+// the odd-block fallback reads through it).
 template <uint32_t T>
 struct Fmt;
 template <>
 struct Fmt<T_Q4_K> {
   using Raw = Q4KRaw;
-  static constexpr int B = 8;
-  static __device__ __forceinline__ Raw load(const uint8_t* row, int it, bool) { return q4k_load(row, it); }
-  static __device__ __forceinline__ float dot(const Raw& r, const uint8_t*, int it, const XLds& X, bool) {
-    return q4k_dot(r, it, X);
+  static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool) { return q4k_load(r, row, it); }
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t*, int it, const XLds& X, bool) {
+    return q4k_dot(w, it, X);
   }
 };
 template <>
 struct Fmt<T_Q6_K> {
   using Raw = Q6KRaw;
-  static constexpr int B = 6;
-  static __device__ __forceinline__ Raw load(const uint8_t* row, int it, bool) { return q6k_load(row, it); }
-  static __device__ __forceinline__ float dot(const Raw& r, const uint8_t*, int it, const XLds& X, bool) {
-    return q6k_dot(r, it, X);
+  static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool) { return q6k_load(r, row, it); }
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t row, const uint8_t*, int it, const XLds& X,
+                                              bool) {
+    return q6k_dot(w, row, it, X);
   }
 };
 template <>
 struct Fmt<T_Q8_0> {
   using Raw = Q8PairRaw;
-  static constexpr int B = 4;
-  static __device__ __forceinline__ Raw load(const uint8_t* row, int it, bool pairs) {
-    Raw r;
-    if (pairs) r = q8_0_pair_load(row, it);
-    return r;
+  static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool pairs) {
+    return q8_0_pair_load(r, pairs ? row : BUF_INVALID, it);
   }
-  static __device__ __forceinline__ float dot(const Raw& r, const uint8_t* row, int it, const XLds& X, bool pairs) {
-    return pairs ? q8_0_pair_dot(r, it, X) : small_block_item(T_Q8_0, row, it, X.xf);
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t* rowp, int it, const XLds& X,
+                                              bool pairs) {
+    if (pairs) return q8_0_pair_dot(w, it, X);
+    return rowp ? small_block_item(T_Q8_0, rowp, it, X.xf) : 0.f;
   }
 };
 template <>
 struct Fmt<T_Q5_0> {
   using Raw = Q5PairRaw;
-  static constexpr int B = 4;
-  static __device__ __forceinline__ Raw load(const uint8_t* row, int it, bool pairs) {
-    Raw r;
-    if (pairs) r = q5_0_pair_load(row, it);
-    return r;
+  static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool pairs) {
+    return q5_0_pair_load(r, pairs ? row : BUF_INVALID, it);
   }
-  static __device__ __forceinline__ float dot(const Raw& r, const uint8_t* row, int it, const XLds& X, bool pairs) {
-    return pairs ? q5_0_pair_dot(r, it, X.xf) : small_block_item(T_Q5_0, row, it, X.xf);
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t* rowp, int it, const XLds& X,
+                                              bool pairs) {
+    if (pairs) return q5_0_pair_dot(w, it, X.xf);
+    return rowp ? small_block_item(T_Q5_0, rowp, it, X.xf) : 0.f;
   }
 };
 struct F32Raw {
-  float4 w[4];
+  uint4 w[4];
 };
 template <>
 struct Fmt<T_F32> {  // 16 floats per item
   using Raw = F32Raw;
-  static constexpr int B = 4;
-  static __device__ __forceinline__ Raw load(const uint8_t* row, int it, bool) {
-    Raw r;
-    const float4* w = (const float4*)row + it * 4;
+  static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool) {
+    Raw o;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.w[i] = w[i];
-    return r;
+    for (int i = 0; i < 4; ++i) o.w[i] = bl128(r, row + 64u * (uint32_t)it + 16u * i);
+    return o;
   }
-  static __device__ __forceinline__ float dot(const Raw& r, const uint8_t*, int it, const XLds& X, bool) {
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t*, int it, const XLds& X, bool) {
     const float4* Xp = (const float4*)X.xf + it * 4;
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float4 b = Xp[i];
-      s += r.w[i].x * b.x + r.w[i].y * b.y + r.w[i].z * b.z + r.w[i].w * b.w;
+      s += __uint_as_float(w.w[i].x) * b.x + __uint_as_float(w.w[i].y) * b.y + __uint_as_float(w.w[i].z) * b.z +
+           __uint_as_float(w.w[i].w) * b.w;
     }
     return s;
   }
 };
 
 // ---- activation staging ------------------------------------------------------
-// Async global -> LDS copy of n floats (n % 4 == 0): each wave instruction
-// moves 64 x 16 B with global_load_lds_dwordx4, so staging costs one memory
-// latency however long the vector is, and no VGPRs.  Caller waits + syncs.
-__device__ __forceinline__ void lds_copy_issue(const float* __restrict__ src, float* dst, uint32_t n) {
-  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n16 = n / 4;
-  for (uint32_t base = wave * 64; base < n16; base += 256)
-    if (base + lane < n16)
-      __builtin_amdgcn_global_load_lds((const void*)(src + 4 * (base + lane)),
-                                       (__attribute__((address_space(3))) void*)(dst + 4 * base), 16, 0, 0);
+// Thread t owns the 8-value groups u = t + 256 i (i < NX) of x.  Their loads
+// (and the rmsnorm gain's) are issued first, before any weight load, so the
+// staging waits only on them while the first weight batch stays in flight.
+__device__ __forceinline__ float4 u4f(uint4 v) {
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
 }
-
-// After the copies of x (and the rmsnorm gain) have landed: apply rmsnorm
-// (tensor.rs:164-185: x * (1 / sqrt(mean(x^2) + eps)) * w) in place, then
-// split every 32-value chunk into the int8 digit planes + metadata that the
-// quantized items read (see XLds in formats.hpp).  Each thread handles 8
-// consecutive values; the 4 threads of a chunk are adjacent lanes.
-__device__ __forceinline__ void stage_finish(uint32_t K, bool norm, float eps, float* xf, const float* nw,
-                                             uint8_t* pl, float* red4) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  float inv = 1.0f;
-  if (norm) {
-    float ss = 0.f;
-    for (uint32_t i = threadIdx.x * 4; i < K; i += 1024) {
-      float4 v = *(const float4*)(xf + i);
-      ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
-    ss = block_sum256(ss, red4);
-    inv = 1.0f / sqrtf(ss / (float)K + eps);
-  }
-  const uint32_t n16 = K / 16;
-  for (uint32_t u0 = 0; u0 < K / 8; u0 += 256) {  // uniform trip count: the shuffles need whole groups
-    const uint32_t u = u0 + threadIdx.x;
-    const bool live = u < K / 8;
-    float v[8];
-    float4* p = (float4*)(xf + 8 * (live ? u : 0));
-    float4 a = p[0], b = p[1];
-    if (norm && live) {
-      const float4* w = (const float4*)(nw + 8 * u);
-      float4 wa = w[0], wb = w[1];
-      a.x = a.x * inv * wa.x; a.y = a.y * inv * wa.y; a.z = a.z * inv * wa.z; a.w = a.w * inv * wa.w;
-      b.x = b.x * inv * wb.x; b.y = b.y * inv * wb.y; b.z = b.z * inv * wb.z; b.w = b.w * inv * wb.w;
-      p[0] = a;
-      p[1] = b;
-    }
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    float amax = 0.f, xsum = 0.f;
+template <int NX, bool NORM>
+struct XStage {
+  float4 x[NX][2], w[NORM ? NX : 1][2];
+  __device__ __forceinline__ void load(rsrc_t rx, rsrc_t rn) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      amax = fmaxf(amax, fabsf(v[i]));
-      xsum += v[i];
-    }
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 4));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 4));  // over the 32-value chunk
-    const float inv_s = amax > 0.f ? 127.0f / amax : 0.f;
-    const float cs = amax > 0.f ? (1.0f / inv_s) * (1.0f / 16384.0f) : 0.f;
-    uint32_t w0[2] = {0, 0}, w1[2] = {0, 0}, w2[2] = {0, 0};
-    int s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float t = v[i] * inv_s;
-      float r0 = rintf(t), e0 = (t - r0) * 128.0f;
-      float r1 = rintf(e0), e1 = (e0 - r1) * 128.0f;
-      float r2 = rintf(e1);
-      int d0 = (int)r0, d1 = (int)r1, d2 = (int)r2;
-      w0[i >> 2] |= (uint32_t)(d0 & 0xFF) << (8 * (i & 3));
-      w1[i >> 2] |= (uint32_t)(d1 & 0xFF) << (8 * (i & 3));
-      w2[i >> 2] |= (uint32_t)(d2 & 0xFF) << (8 * (i & 3));
-      s0 += d0;
-      s1 += d1;
-      s2 += d2;
-    }
-    // per 16-value record: the two threads u, u^1
-    xsum += __shfl_xor(xsum, 1, 2);
-    s0 += __shfl_xor(s0, 1, 2);
-    s1 += __shfl_xor(s1, 1, 2);
-    s2 += __shfl_xor(s2, 1, 2);
-    if (live) {
-      const uint32_t c = u >> 1, off = 16u * swz(c, n16) + 8u * (u & 1);
-      *(uint2*)(pl + off) = make_uint2(w0[0], w0[1]);
-      *(uint2*)(pl + K + off) = make_uint2(w1[0], w1[1]);
-      *(uint2*)(pl + 2 * K + off) = make_uint2(w2[0], w2[1]);
-      if ((u & 1) == 0)
-        *(float4*)(pl + 3 * K + 16u * swz(c, n16)) =
-            make_float4(cs, xsum, __int_as_float(s0), __int_as_float(128 * s1 + s2));
+    for (int i = 0; i < NX; ++i) {
+      const uint32_t o = 32u * (threadIdx.x + 256u * i);
+      x[i][0] = u4f(bl128(rx, o));
+      x[i][1] = u4f(bl128(rx, o + 16u));
+      if (NORM) {
+        w[i][0] = u4f(bl128(rn, o));
+        w[i][1] = u4f(bl128(rn, o + 16u));
+      }
     }
   }
-  __syncthreads();
-}
+  // rmsnorm (tensor.rs:164-185: x * (1 / sqrt(mean(x^2) + eps)) * w) when
+  // norm, then split every 32-value chunk into the int8 digit planes and
+  // metadata the quantized items read (XLds in formats.hpp) and keep the
+  // f32 values for the f32 items.  The 4 threads of a chunk are adjacent
+  // lanes; groups past K were loaded as zeros and are not stored.
+  __device__ __forceinline__ void finish(uint32_t K, bool norm, float eps, float* xf, uint8_t* pl, float* red4) {
+    float inv = 1.0f;
+    if (NORM && norm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < NX; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) ss += x[i][h].x * x[i][h].x + x[i][h].y * x[i][h].y + x[i][h].z * x[i][h].z +
+                                          x[i][h].w * x[i][h].w;
+      ss = block_sum256(ss, red4);
+      inv = 1.0f / sqrtf(ss / (float)K + eps);
+    }
+    const uint32_t n16 = K / 16;
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      if (256u * i >= K / 8) break;  // block-uniform: no thread has group i
+      const uint32_t u = threadIdx.x + 256u * i;
+      const bool live = u < K / 8;
+      float4 a = x[i][0], b = x[i][1];
+      if (NORM && norm) {
+        const float4 wa = w[i][0], wb = w[i][1];
+        a.x = a.x * inv * wa.x; a.y = a.y * inv * wa.y; a.z = a.z * inv * wa.z; a.w = a.w * inv * wa.w;
+        b.x = b.x * inv * wb.x; b.y = b.y * inv * wb.y; b.z = b.z * inv * wb.z; b.w = b.w * inv * wb.w;
+      }
+      if (live) {
+        ((float4*)xf)[2 * u] = a;
+        ((float4*)xf)[2 * u + 1] = b;
+      }
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      float amax = 0.f, xsum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        amax = fmaxf(amax, fabsf(v[j]));
+        xsum += v[j];
+      }
+      amax = fmaxf(amax, __shfl_xor(amax, 1, 4));
+      amax = fmaxf(amax, __shfl_xor(amax, 2, 4));  // over the 32-value chunk
+      const float inv_s = amax > 0.f ? 127.0f / amax : 0.f;
+      const float cs = amax > 0.f ? (1.0f / inv_s) * (1.0f / 16384.0f) : 0.f;
+      uint32_t w0[2] = {0, 0}, w1[2] = {0, 0}, w2[2] = {0, 0};
+      int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float t = v[j] * inv_s;
+        float r0 = rintf(t), e0 = (t - r0) * 128.0f;
+        float r1 = rintf(e0), e1 = (e0 - r1) * 128.0f;
+        float r2 = rintf(e1);
+        int d0 = (int)r0, d1 = (int)r1, d2 = (int)r2;
+        w0[j >> 2] |= (uint32_t)(d0 & 0xFF) << (8 * (j & 3));
+        w1[j >> 2] |= (uint32_t)(d1 & 0xFF) << (8 * (j & 3));
+        w2[j >> 2] |= (uint32_t)(d2 & 0xFF) << (8 * (j & 3));
+        s0 += d0;
+        s1 += d1;
+        s2 += d2;
+      }
+      // per 16-value record: the two threads u, u^1
+      xsum += __shfl_xor(xsum, 1, 2);
+      s0 += __shfl_xor(s0, 1, 2);
+      s1 += __shfl_xor(s1, 1, 2);
+      s2 += __shfl_xor(s2, 1, 2);
+      if (live) {
+        const uint32_t c = u >> 1, off = 16u * swz(c, n16) + 8u * (u & 1);
+        *(uint2*)(pl + off) = make_uint2(w0[0], w0[1]);
+        *(uint2*)(pl + K + off) = make_uint2(w1[0], w1[1]);
+        *(uint2*)(pl + 2 * K + off) = make_uint2(w2[0], w2[1]);
+        if ((u & 1) == 0)
+          *(float4*)(pl + 3 * K + 16u * swz(c, n16)) =
+              make_float4(cs, xsum, __int_as_float(s0), __int_as_float(128 * s1 + s2));
+      }
+    }
+    __syncthreads();
+  }
+};
 
 __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
   if (v == 0.0f) v = 0.0f;  // -0 and +0 compare equal in the reference
@@ -231,70 +246,87 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
 
 // ---- fused dequant-GEMV -----------------------------------------------------------
 // A block stages x (and applies the rmsnorm) once; then each of its 4 waves
-// works alone through "units" of 64 / LPR rows, one group of LPR lanes per
-// row (SWIGLU: per gate/up row pair).  Wave w of block b takes units
-// 4b + w, 4b + w + 4 * nblk, ...  Lane gl owns items gl, gl + LPR, ... of
-// its row; the loads of the next unit are issued before the current one is
-// computed (double buffer), and the first unit's loads before the staging.
-template <uint32_t T, int LPR, int MODE>
-struct Gemv {
+// works alone through "units" of G = 64 / LPR rows, one group of LPR lanes
+// per row (SWIGLU: per gate/up row pair).  Wave w of block b takes units
+// 4b + w, 4b + w + 4 * nblk, ...  A unit is S steps; in step s lane gl of a
+// row loads items (s * BI + j) * LPR + gl, j < BI.  The steps of all the
+// wave's units form one flat pipeline: the loads of step f + 1 are issued
+// before step f is computed, and the first step's before the staging.
+template <uint32_t T, int LPR, int MODE, int NX, bool NORM>
+__device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, uint32_t blk, uint32_t nblk,
+                                          float* xf, uint8_t* pl, float* red4, uint64_t* best_s) {
   using F = Fmt<T>;
   using Raw = typename F::Raw;
-  static constexpr int B = F::B;
-  static constexpr int R = MODE == GEMV_SWIGLU ? 2 : 1;
-  static constexpr int G = 64 / LPR;  // rows per unit
-  static_assert(B % R == 0, "batch must hold whole row groups");
+  constexpr int R = MODE == GEMV_SWIGLU ? 2 : 1;
+  constexpr int BI = gemv_bi(T, MODE), B = BI * R, G = 64 / LPR;
+  constexpr bool EX = MODE == GEMV_STORE || MODE == GEMV_RESID;  // per-row bias / residual input
+  // the wave index through readfirstlane: the compiler then knows every
+  // per-wave quantity below is uniform (scalar loop control, no exec masks)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gl = lane % LPR, g = lane / LPR;
+  const bool pr = ((a.in / 32) % 2) == 0;
+  const int n_items = items_per_row(T, a.in, pr);
+  const uint32_t S = (uint32_t)(n_items + LPR * BI - 1) / (LPR * BI);
+  const uint32_t n_units = (sg.rows + G - 1) / G, stride = 4 * nblk, u0 = 4 * blk + wave;
+  const uint32_t n_steps = u0 < n_units ? (n_units - u0 + stride - 1) / stride * S : 0;
+  const uint32_t wbytes = sg.rows * sg.row_bytes;
+  const rsrc_t rw = make_rsrc(sg.w, wbytes), rw2 = make_rsrc(R == 2 ? sg.w2 : sg.w, wbytes);
+  const float* exp_ = MODE == GEMV_RESID ? sg.resid : sg.bias;
+  const rsrc_t rex = make_rsrc(exp_, exp_ ? sg.rows * 4 : 0);
+  const XLds X{xf, pl, a.in};
 
-  const GemvArgs& a;
-  const GemvSeg& sg;
-  const XLds& X;
-  int gl, g;
-  bool pr;
-  int n_items;
+  XStage<NX, NORM> xs;
+  xs.load(make_rsrc(a.x, a.in * 4), make_rsrc(a.norm_w, a.norm_w ? a.in * 4 : 0));
+  __builtin_amdgcn_sched_barrier(0);  // keep the x loads ahead of the weight loads
 
-  __device__ __forceinline__ uint32_t row_of(uint32_t unit) const { return unit * G + g; }
-  __device__ __forceinline__ int work(uint32_t row) const {
-    return (row < sg.rows && gl < n_items) ? (n_items - gl + LPR - 1) / LPR * R : 0;
-  }
-  __device__ __forceinline__ const uint8_t* wrow(uint32_t row, int r) const {
-    return (r == 0 ? sg.w : sg.w2) + (size_t)row * sg.row_bytes;
-  }
-  __device__ __forceinline__ int issue(uint32_t unit, Raw (&raw)[B]) const {
-    const uint32_t row = row_of(unit);
-    const int n = work(row), nb = n < B ? n : B;
+  auto row_off = [&](uint32_t unit) -> uint32_t {
+    const uint32_t row = unit * G + g;
+    return row < sg.rows ? row * sg.row_bytes : BUF_INVALID;
+  };
+  // the bias / residual of the row rides along with the unit's last step,
+  // so the epilogue issues no load of its own (which would have to wait for
+  // the next step's loads too)
+  auto issue = [&](uint32_t unit, uint32_t step, Raw(&raw)[B], float& ex) {
+    const uint32_t ro = row_off(unit);
 #pragma unroll
-    for (int b = 0; b < B; ++b)
-      if (b < nb) raw[b] = F::load(wrow(row, b % R), gl + (b / R) * LPR, pr);
-    return nb;
-  }
-  // consume a unit whose first batch is in raw; returns the row's results
-  __device__ __forceinline__ void compute(uint32_t unit, Raw (&raw)[B], int nb, uint64_t& best) const {
-    const uint32_t row = row_of(unit);
-    const int n_work = work(row);
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.f;
-    int k0 = 0;
-    while (nb > 0) {
-#pragma unroll
-      for (int b = 0; b < B; ++b)
-        if (b < nb) acc[b % R] += F::dot(raw[b], wrow(row, b % R), gl + ((k0 + b) / R) * LPR, X, pr);
-      k0 += nb;
-      nb = n_work - k0 < B ? n_work - k0 : B;
-#pragma unroll
-      for (int b = 0; b < B; ++b)  // rows longer than one batch: further batches, not prefetched
-        if (b < nb) raw[b] = F::load(wrow(row, b % R), gl + ((k0 + b) / R) * LPR, pr);
+    for (int j = 0; j < BI; ++j) {
+      const int it = (int)(step * BI + j) * LPR + gl;
+      const uint32_t o = it < n_items ? ro : BUF_INVALID;
+      raw[j * R] = F::load(rw, o, it, pr);
+      if (R == 2) raw[j * R + R - 1] = F::load(rw2, o, it, pr);
     }
+    if (EX) ex = __uint_as_float(bl32(rex, ro == BUF_INVALID ? BUF_INVALID : 4u * (unit * G + g)));
+  };
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  uint64_t best = 0;
+  auto consume = [&](uint32_t unit, uint32_t step, Raw(&raw)[B], float ex) {
+    const uint32_t row = unit * G + g, ro = row_off(unit);
+#pragma unroll
+    for (int j = 0; j < BI; ++j) {
+      const int it = (int)(step * BI + j) * LPR + gl;
+      const bool ok = it < n_items && ro != BUF_INVALID;
+      const int itc = ok ? it : 0;  // masked items read chunk 0 of x and have zero weights
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint8_t* rp = ok ? (r == 0 ? sg.w : sg.w2) + ro : nullptr;
+        acc[r] += F::dot(raw[j * R + r], ro, rp, itc, X, pr);
+      }
+    }
+    if (step + 1 < S) return;
     float acc0 = acc[0], acc1 = acc[R - 1];
 #pragma unroll
     for (int o = LPR / 2; o > 0; o >>= 1) {
       acc0 += __shfl_xor(acc0, o, LPR);
       if (MODE == GEMV_SWIGLU) acc1 += __shfl_xor(acc1, o, LPR);
     }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
     if (gl == 0 && row < sg.rows) {
-      if (MODE == GEMV_STORE) sg.out[row] = sg.bias ? acc0 + sg.bias[row] : acc0;  // model.rs:179-183
+      if (MODE == GEMV_STORE) sg.out[row] = sg.bias ? acc0 + ex : acc0;  // model.rs:179-183
       if (MODE == GEMV_RESID) {
-        float v = sg.resid[row] + acc0;  // tensor.rs:232
+        float v = ex + acc0;  // tensor.rs:232
         sg.out[row] = v;
         if (sg.out2) sg.out2[row] = v;
       }
@@ -305,35 +337,31 @@ struct Gemv {
         best = kk > best ? kk : best;
       }
     }
-  }
-};
+  };
 
-template <uint32_t T, int LPR, int MODE>
-__device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, uint32_t blk, uint32_t nblk, float* xs,
-                                          float* nw, uint8_t* pl, float* red4, uint64_t* best_s) {
-  using W = Gemv<T, LPR, MODE>;
-  const XLds X{xs, pl, a.in};
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool pr = ((a.in / 32) % 2) == 0;
-  const W w{a, sg, X, lane % LPR, lane / LPR, pr, items_per_row(T, a.in, pr)};
-  const uint32_t n_units = (sg.rows + W::G - 1) / W::G, stride = 4 * nblk;
-  uint32_t unit = 4 * blk + wave;
-  typename W::Raw ra[W::B], rb[W::B];
-  int na = unit < n_units ? w.issue(unit, ra) : 0, nb = 0;
-  lds_copy_issue(a.x, xs, a.in);
-  if (a.norm_w) lds_copy_issue(a.norm_w, nw, a.in);
-  stage_finish(a.in, a.norm_w != nullptr, a.eps, xs, nw, pl, red4);
-  uint64_t best = 0;
-  while (unit < n_units) {  // per-wave loop, unrolled by two for the double buffer
-    uint32_t next = unit + stride;
-    if (next < n_units) nb = w.issue(next, rb);
-    w.compute(unit, ra, na, best);
-    unit = next;
-    if (unit >= n_units) break;
-    next = unit + stride;
-    if (next < n_units) na = w.issue(next, ra);
-    w.compute(unit, rb, nb, best);
-    unit = next;
+  Raw ra[B], rb[B];
+  float ea = 0.f, eb = 0.f;
+  uint32_t iu = u0, is = 0, cu = u0, cs = 0;
+  auto next = [&](uint32_t& u, uint32_t& s) {
+    if (++s == S) {
+      s = 0;
+      u += stride;
+    }
+  };
+  issue(iu, is, ra, ea);
+  next(iu, is);
+  __builtin_amdgcn_sched_barrier(0);
+  xs.finish(a.in, a.norm_w != nullptr, a.eps, xf, pl, red4);
+  for (uint32_t f = 0; f < n_steps; f += 2) {
+    issue(iu, is, rb, eb);  // past the wave's last step: rows past the end, loads of zeros
+    next(iu, is);
+    consume(cu, cs, ra, ea);
+    next(cu, cs);
+    if (f + 1 >= n_steps) break;
+    issue(iu, is, ra, ea);
+    next(iu, is);
+    consume(cu, cs, rb, eb);
+    next(cu, cs);
   }
   if (MODE == GEMV_ARGMAX) {
     for (int o = 32; o > 0; o >>= 1) {
@@ -352,49 +380,64 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
 
 // T0 serves every segment whose type is T0, T1 the others (T1 == T0 for
 // single-format launches), so each kernel carries one or two format paths.
-template <uint32_t T0, uint32_t T1, int LPR, int MODE>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+// NX: 8-value groups of x per thread (in <= 2048 * NX); NORM: rmsnorm
+// support (only the small-in kernels, where the norms occur).
+template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX>
+__global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
+  constexpr bool NORM = NX <= 2;
   extern __shared__ float4 smem4[];
   __shared__ float red4[4];
   __shared__ uint64_t best_s[4];
-  // LDS: x[in] f32 | 4 byte planes of in bytes (digits, metadata) | norm gain[in] (only with a norm)
-  float* xs = (float*)smem4;
-  uint8_t* pl = (uint8_t*)(xs + a.in);
-  float* nw = (float*)(pl + 4 * (size_t)a.in);
+  // LDS: x[in] f32 | 4 byte planes of in bytes (digits, metadata)
+  float* xf = (float*)smem4;
+  uint8_t* pl = (uint8_t*)(xf + a.in);
   int si = 0;
   while (si + 1 < a.n_seg && blockIdx.x >= a.seg[si + 1].block0) ++si;
   const GemvSeg& sg = a.seg[si];
   const uint32_t blk = blockIdx.x - sg.block0;
   const uint32_t nblk = (si + 1 < a.n_seg ? a.seg[si + 1].block0 : gridDim.x) - sg.block0;
   if (T0 == T1 || sg.type == T0)
-    gemv_body<T0, LPR, MODE>(a, sg, blk, nblk, xs, nw, pl, red4, best_s);
+    gemv_body<T0, LPR, MODE, NX, NORM>(a, sg, blk, nblk, xf, pl, red4, best_s);
   else
-    gemv_body<T1, LPR, MODE>(a, sg, blk, nblk, xs, nw, pl, red4, best_s);
+    gemv_body<T1, LPR, MODE, NX, NORM>(a, sg, blk, nblk, xf, pl, red4, best_s);
 }
 
-size_t gemv_lds_bytes(uint32_t in, bool norm) { return (size_t)in * (4 + 4 + (norm ? 4 : 0)); }
+size_t gemv_lds_bytes(uint32_t in, bool) { return (size_t)in * 8; }
 
-// Lanes per row: 16 when the launch has enough rows to fill the GPU with
-// groups of 16 rows, else 32 or 64 so small matrices still spread over the
-// 256 CUs -- but never so many that most lanes of a group sit idle.
-static int lanes_per_row(uint32_t total_rows, int n_items) {
-  int lpr = total_rows >= 8192 ? 16 : total_rows >= 4096 ? 32 : 64;
-  while (lpr > 16 && n_items <= lpr / 2) lpr /= 2;
-  return lpr;
+
+// Lanes per row: the choice in {16, 32, 64} that keeps the most lanes busy
+// on real items, counting at most the 2048 waves that are resident at once
+// (ties: fewer lanes, so fewer blocks stage x).
+static int lanes_per_row(uint32_t total_rows, uint32_t type, int mode, int n_items) {
+  int best_l = 16;
+  double best_score = -1.0;
+  for (int l = 16; l <= 64; l *= 2) {
+    double waves = (double)total_rows * l / 64.0;
+    if (waves > 2048.0) waves = 2048.0;
+    int slots = l * gemv_bi(type, mode);
+    int steps = (n_items + slots - 1) / slots;
+    double eff = steps ? (double)n_items / ((double)slots * steps) : 0.0;
+    double score = waves * eff;
+    if (score > best_score * 1.05) {
+      best_score = score;
+      best_l = l;
+    }
+  }
+  return best_l;
 }
 
-constexpr uint32_t GEMV_MAX_BLOCKS = 512;  // 2 resident blocks (8 waves) per CU
+static uint32_t max_blocks(uint32_t in) { return gemv_lds_bytes(in, false) > 80 * 1024 ? 256 : 512; }
 
 // Blocks per segment in proportion to its units of 64 / LPR rows; each
-// block runs 4 wave workers.
+// block runs 4 wave workers; at most as many blocks as are resident at once.
 static uint32_t plan_blocks(GemvArgs& a, uint32_t rows_per_unit) {
-  uint32_t want[3], total = 0;
+  uint32_t want[3], total = 0, cap = max_blocks(a.in);
   for (int i = 0; i < a.n_seg; ++i) {
     uint32_t units = (a.seg[i].rows + rows_per_unit - 1) / rows_per_unit;
     want[i] = (units + 3) / 4;
     total += want[i];
   }
-  uint32_t grid = total < GEMV_MAX_BLOCKS ? total : GEMV_MAX_BLOCKS, used = 0;
+  uint32_t grid = total < cap ? total : cap, used = 0;
   for (int i = 0; i < a.n_seg; ++i) {
     uint32_t b = i + 1 == a.n_seg ? grid - used : (uint32_t)(((uint64_t)grid * want[i] + total / 2) / total);
     if (b < 1) b = 1;
@@ -406,29 +449,38 @@ static uint32_t plan_blocks(GemvArgs& a, uint32_t rows_per_unit) {
 }
 
 uint32_t gemv_blocks(uint32_t type, uint32_t rows, uint32_t in) {
-  int lpr = lanes_per_row(rows, items_per_row(type, in, ((in / 32) % 2) == 0));
-  uint32_t units = (rows + 64 / lpr - 1) / (64 / lpr), want = (units + 3) / 4;
-  return want < GEMV_MAX_BLOCKS ? want : GEMV_MAX_BLOCKS;
+  int lpr = lanes_per_row(rows, type, GEMV_STORE, items_per_row(type, in, ((in / 32) % 2) == 0));
+  uint32_t units = (rows + 64 / lpr - 1) / (64 / lpr), want = (units + 3) / 4, cap = max_blocks(in);
+  return want < cap ? want : cap;
 }
 
-template <uint32_t T0, uint32_t T1, int LPR, int MODE>
+template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX>
 static hipError_t go(GemvArgs a, hipStream_t s, uint32_t* nblocks) {
   uint32_t total = plan_blocks(a, 64 / LPR);
   if (nblocks) *nblocks = total;
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL((k_gemv<T0, T1, LPR, MODE>), dim3(total), dim3(256), gemv_lds_bytes(a.in, a.norm_w != nullptr),
-                     s, a);
+  hipLaunchKernelGGL((k_gemv<T0, T1, LPR, MODE, NX>), dim3(total), dim3(256), gemv_lds_bytes(a.in, false), s, a);
   return hipGetLastError();
+}
+
+// in <= 4096 (the hidden-size inputs, with or without rmsnorm) or, without
+// rmsnorm and only for STORE/RESID, in <= 20480 (the FFN down projection).
+template <uint32_t T0, uint32_t T1, int MODE, int LPR>
+static hipError_t pick_nx(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
+  if (a.in <= 4096) return go<T0, T1, LPR, MODE, 2>(a, s, nb);
+  if constexpr (MODE == GEMV_STORE || MODE == GEMV_RESID)
+    if (a.norm_w == nullptr && a.in <= 20480) return go<T0, T1, LPR, MODE, 10>(a, s, nb);
+  return hipErrorInvalidValue;
 }
 
 template <uint32_t T0, uint32_t T1, int MODE>
 static hipError_t pick_lpr(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
   uint32_t rows = 0;
   for (int i = 0; i < a.n_seg; ++i) rows += a.seg[i].rows;
-  int lpr = lanes_per_row(rows, items_per_row(a.seg[0].type, a.in, ((a.in / 32) % 2) == 0));
-  if (lpr == 16) return go<T0, T1, 16, MODE>(a, s, nb);
-  if (lpr == 32) return go<T0, T1, 32, MODE>(a, s, nb);
-  return go<T0, T1, 64, MODE>(a, s, nb);
+  int lpr = lanes_per_row(rows, a.seg[0].type, MODE, items_per_row(a.seg[0].type, a.in, ((a.in / 32) % 2) == 0));
+  if (lpr == 16) return pick_nx<T0, T1, MODE, 16>(a, s, nb);
+  if (lpr == 32) return pick_nx<T0, T1, MODE, 32>(a, s, nb);
+  return pick_nx<T0, T1, MODE, 64>(a, s, nb);
 }
 
 template <int MODE>
@@ -469,6 +521,8 @@ static hipError_t launch_split(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
 }
 
 hipError_t launch_gemv(GemvArgs a, GemvMode mode, hipStream_t s, uint32_t* nb) {
+  for (int i = 0; i < a.n_seg; ++i)  // buffer offsets are 32-bit with BUF_INVALID above the range
+    if ((uint64_t)a.seg[i].rows * a.seg[i].row_bytes >= BUF_INVALID) return hipErrorInvalidValue;
   switch (mode) {
     case GEMV_STORE: return launch_split<GEMV_STORE>(a, s, nb);
     case GEMV_RESID: return launch_split<GEMV_RESID>(a, s, nb);
@@ -481,10 +535,13 @@ hipError_t launch_gemv(GemvArgs a, GemvMode mode, hipStream_t s, uint32_t* nb) {
 template <uint32_t T0, uint32_t T1, int LPR>
 static hipError_t prep_one(int bytes) {
   hipError_t e;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes))) return e;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes))) return e;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_SWIGLU>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes))) return e;
-  return hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_ARGMAX>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  const auto attr = hipFuncAttributeMaxDynamicSharedMemorySize;
+  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 2>, attr, bytes))) return e;
+  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 2>, attr, bytes))) return e;
+  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_SWIGLU, 2>, attr, bytes))) return e;
+  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_ARGMAX, 2>, attr, bytes))) return e;
+  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 10>, attr, bytes))) return e;
+  return hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 10>, attr, bytes);
 }
 
 template <uint32_t T0, uint32_t T1>
