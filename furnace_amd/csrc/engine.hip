@@ -70,11 +70,10 @@ struct frn_ctx {
   std::vector<LayerPtrs> layers;
   const DevTensor *embd = nullptr, *lm_head = nullptr;
   const float* out_norm = nullptr;
-  float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *act = nullptr, *logits = nullptr;
+  float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *act = nullptr, *logits = nullptr;
   float *part = nullptr, *kcache = nullptr, *vcache = nullptr, *rope = nullptr;
   uint64_t* best_part = nullptr;  // per-block argmax candidates of the lm_head kernel
   uint32_t n_best = 0;
-  uint32_t* att_count = nullptr;  // per kv head: attention splits finished (zero between launches)
   StepState* st = nullptr;
   StepState* h_st = nullptr;  // pinned mirror for read-back
   uint32_t len = 0;           // host view of KvCache::len
@@ -98,7 +97,7 @@ static void free_ctx(frn_ctx* c) {
   if (c->graph_prefill) (void)hipGraphDestroy(c->graph_prefill);
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->att, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part, c->att_count};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -121,8 +120,8 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
     return fail(FRN_ESHAPE, "frn_create: head_dim %u != hidden %u / n_heads %u", c.head_dim, c.hidden, c.n_heads);
   if (c.n_heads % c.n_kv_heads) return fail(FRN_ESHAPE, "frn_create: %u heads not divisible by %u kv heads", c.n_heads, c.n_kv_heads);
   if (c.head_dim != 64 && c.head_dim != 128) return fail(FRN_ESHAPE, "frn_create: head_dim %u unsupported (64, 128)", c.head_dim);
-  if (c.n_heads / c.n_kv_heads > (c.head_dim == 64 ? 16u : 8u))
-    return fail(FRN_ESHAPE, "frn_create: %u query heads per kv head unsupported", c.n_heads / c.n_kv_heads);
+  if (!attention_supported(c.n_heads, c.n_kv_heads, c.head_dim))
+    return fail(FRN_ESHAPE, "frn_create: %u query heads per kv head unsupported (at most 8)", c.n_heads / c.n_kv_heads);
   // activation vectors are staged with 16-byte loads in 16-value chunks;
   // per-format block divisibility is checked per tensor at upload/finalize
   if (c.hidden % 32 || c.ffn % 32) return fail(FRN_ESHAPE, "frn_create: hidden and ffn must be multiples of 32");
@@ -143,13 +142,12 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
   hipError_t e;
   if ((e = hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking)) || (e = dmalloc(&x->x, c.hidden * 4)) ||
       (e = dmalloc(&x->q, qd * 4)) || (e = dmalloc(&x->k, kvd * 4)) || (e = dmalloc(&x->v, kvd * 4)) ||
-      (e = dmalloc(&x->att, qd * 4)) || (e = dmalloc(&x->act, (size_t)c.ffn * 4)) ||
+      (e = dmalloc(&x->act, (size_t)c.ffn * 4)) ||
       (e = dmalloc(&x->logits, (size_t)c.vocab * 4)) ||
       (e = dmalloc(&x->part, attention_part_floats(c.n_heads, c.head_dim, c.max_ctx) * 4)) ||
       (e = dmalloc(&x->kcache, kv_bytes)) || (e = dmalloc(&x->vcache, kv_bytes)) ||
       (e = dmalloc(&x->rope, (size_t)c.max_ctx * c.head_dim * 4)) || (e = dmalloc(&x->st, sizeof(StepState))) ||
       (e = dmalloc(&x->best_part, ((size_t)c.vocab + 3) / 4 * 8)) ||  // >= lm_head blocks (4+ rows each)
-      (e = dmalloc(&x->att_count, (size_t)c.n_kv_heads * 4)) ||
       (e = hipHostMalloc((void**)&x->h_st, sizeof(StepState), hipHostMallocDefault))) {
     free_ctx(x);
     return hip_fail(e, "frn_create: allocation");
@@ -168,7 +166,6 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
     }
   StepState init{};
   if ((e = hipMemcpy(x->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice)) ||
-      (e = hipMemset(x->att_count, 0, (size_t)c.n_kv_heads * 4)) ||
       (e = hipMemcpy(x->st, &init, sizeof init, hipMemcpyHostToDevice)) ||
       (e = hipMemset(x->kcache, 0, kv_bytes)) || (e = hipMemset(x->vcache, 0, kv_bytes)) ||
       (e = gemv_prepare(std::max(gemv_lds_bytes(c.hidden, true),
@@ -318,13 +315,18 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
     // rope, KV append, attention (model.rs:460-467)
     size_t lo = (size_t)l * g.max_ctx * g.n_kv_heads * g.head_dim;
     if (TIMED(CAT_ATTN, launch_attention(c->q, c->k, c->v, c->rope, c->kcache + lo, c->vcache + lo, g.n_heads,
-                                         g.n_kv_heads, g.head_dim, g.max_ctx, scale, c->part, c->att_count, c->att,
-                                         c->st, s)))
+                                         g.n_kv_heads, g.head_dim, g.max_ctx, scale, c->part, c->st, s)))
       return e;
-    // o-proj + residual (model.rs:469-470)
-    GemvArgs o = args(QD, c->att, nullptr);
+    // merge of the attention splits + o-proj + residual (model.rs:436-438, 469-470)
+    GemvArgs o = args(QD, nullptr, nullptr);
     o.seg[0] = seg(L.wo, nullptr, nullptr, c->x, c->x);
-    if (TIMED(CAT_OPROJ, launch_gemv(o, GEMV_RESID, s))) return e;
+    o.att_part = c->part;
+    o.st = c->st;
+    o.att_ms = attention_splits(g.max_ctx);
+    o.att_hd = g.head_dim;
+    o.att_chunk = ATTENTION_CHUNK;
+    o.att_part_bytes = (uint32_t)(attention_part_floats(g.n_heads, g.head_dim, g.max_ctx) * 4);
+    if (TIMED(CAT_OPROJ, launch_gemv(o, GEMV_RESID_ATT, s))) return e;
     // rmsnorm + gate/up + SwiGLU (model.rs:473-476)
     GemvArgs gu = args(H, c->x, L.ffn_norm);
     gu.seg[0] = seg(L.gate, L.up, nullptr, c->act, nullptr);

@@ -5,7 +5,8 @@
 
 namespace frn {
 
-constexpr int ATT_CHUNK = 64;  // positions per attention block (one wave per softmax row)
+constexpr int ATT_CHUNK = ATTENTION_CHUNK;  // positions per attention block (one wave per softmax row)
+uint32_t attention_splits(uint32_t max_ctx) { return (max_ctx + ATT_CHUNK - 1) / ATT_CHUNK; }
 
 // ---- reductions -----------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
@@ -143,9 +144,69 @@ struct Fmt<T_F32> {  // 16 floats per item
 __device__ __forceinline__ float4 u4f(uint4 v) {
   return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
 }
-template <int NX, bool NORM>
+template <int NX, bool NORM, bool ATT>
 struct XStage {
+  // ATT: x is the attention output, merged here from the per-split partials
+  // (o, m, l) of the attention kernel: NB splits are loaded up front with
+  // the other staging loads, further splits (long contexts) afterwards.
+  static constexpr int NB = ATT ? 8 / NX : 1;
   float4 x[NX][2], w[NORM ? NX : 1][2];
+  float2 pm[ATT ? NX : 1][NB];
+  float4 po[ATT ? NX : 1][NB][2];
+  uint32_t ns = 0;
+  __device__ __forceinline__ uint32_t part_off(const GemvArgs& a, uint32_t u, uint32_t sp) const {
+    const uint32_t h = 8u * u / a.att_hd, d0 = 8u * u % a.att_hd;
+    return 4u * ((h * a.att_ms + sp) * (a.att_hd + 2) + d0);
+  }
+  __device__ __forceinline__ void load_att(const GemvArgs& a, rsrc_t rp) {
+    ns = a.st->pos / a.att_chunk + 1;
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const uint32_t u = threadIdx.x + 256u * i;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint32_t o = (u < a.in / 8 && (uint32_t)b < ns) ? part_off(a, u, b) : BUF_INVALID;
+        po[i][b][0] = u4f(bl128(rp, o));
+        po[i][b][1] = u4f(bl128(rp, o + 16u));
+        const uint2 q = bl64(rp, o == BUF_INVALID ? BUF_INVALID : o - 4u * (8u * u % a.att_hd) + 4u * a.att_hd);
+        pm[i][b] = make_float2(__uint_as_float(q.x), __uint_as_float(q.y));
+      }
+    }
+  }
+  // softmax merge of the splits (model.rs:371-438 evaluated split-wise):
+  // x = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, M = max_s m_s
+  __device__ __forceinline__ void merge_att(const GemvArgs& a, rsrc_t rp) {
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const uint32_t u = threadIdx.x + 256u * i;
+      float M = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        if ((uint32_t)b < ns) M = fmaxf(M, pm[i][b].x);
+      float L = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float e = (uint32_t)b < ns ? expf(pm[i][b].x - M) : 0.f;
+        L += e * pm[i][b].y;
+        o[0] += e * po[i][b][0].x; o[1] += e * po[i][b][0].y; o[2] += e * po[i][b][0].z; o[3] += e * po[i][b][0].w;
+        o[4] += e * po[i][b][1].x; o[5] += e * po[i][b][1].y; o[6] += e * po[i][b][1].z; o[7] += e * po[i][b][1].w;
+      }
+      for (uint32_t sp = NB; sp < ns; ++sp) {  // beyond the first batch: one split at a time
+        const uint32_t off = u < a.in / 8 ? part_off(a, u, sp) : BUF_INVALID;
+        const float4 p0 = u4f(bl128(rp, off)), p1 = u4f(bl128(rp, off + 16u));
+        const uint2 q = bl64(rp, off == BUF_INVALID ? BUF_INVALID : off - 4u * (8u * u % a.att_hd) + 4u * a.att_hd);
+        const float m = __uint_as_float(q.x), l = __uint_as_float(q.y);
+        const float Mn = fmaxf(M, m), c = expf(M - Mn), e = expf(m - Mn);
+        M = Mn;
+        L = L * c + e * l;
+        o[0] = o[0] * c + e * p0.x; o[1] = o[1] * c + e * p0.y; o[2] = o[2] * c + e * p0.z; o[3] = o[3] * c + e * p0.w;
+        o[4] = o[4] * c + e * p1.x; o[5] = o[5] * c + e * p1.y; o[6] = o[6] * c + e * p1.z; o[7] = o[7] * c + e * p1.w;
+      }
+      const float il = L > 0.f ? 1.0f / L : 0.f;
+      x[i][0] = make_float4(o[0] * il, o[1] * il, o[2] * il, o[3] * il);
+      x[i][1] = make_float4(o[4] * il, o[5] * il, o[6] * il, o[7] * il);
+    }
+  }
   __device__ __forceinline__ void load(rsrc_t rx, rsrc_t rn) {
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
@@ -259,7 +320,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   using Raw = typename F::Raw;
   constexpr int R = MODE == GEMV_SWIGLU ? 2 : 1;
   constexpr int BI = gemv_bi(T, MODE), B = BI * R, G = 64 / LPR;
-  constexpr bool EX = MODE == GEMV_STORE || MODE == GEMV_RESID;  // per-row bias / residual input
+  constexpr bool ATT = MODE == GEMV_RESID_ATT;  // x = merged attention partials, then as RESID
+  constexpr bool RES = MODE == GEMV_RESID || ATT;
+  constexpr bool EX = MODE == GEMV_STORE || RES;  // per-row bias / residual input
   // the wave index through readfirstlane: the compiler then knows every
   // per-wave quantity below is uniform (scalar loop control, no exec masks)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -271,12 +334,16 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   const uint32_t n_steps = u0 < n_units ? (n_units - u0 + stride - 1) / stride * S : 0;
   const uint32_t wbytes = sg.rows * sg.row_bytes;
   const rsrc_t rw = make_rsrc(sg.w, wbytes), rw2 = make_rsrc(R == 2 ? sg.w2 : sg.w, wbytes);
-  const float* exp_ = MODE == GEMV_RESID ? sg.resid : sg.bias;
+  const float* exp_ = RES ? sg.resid : sg.bias;
   const rsrc_t rex = make_rsrc(exp_, exp_ ? sg.rows * 4 : 0);
   const XLds X{xf, pl, a.in};
 
-  XStage<NX, NORM> xs;
-  xs.load(make_rsrc(a.x, a.in * 4), make_rsrc(a.norm_w, a.norm_w ? a.in * 4 : 0));
+  XStage<NX, NORM, ATT> xs;
+  const rsrc_t rp = make_rsrc(a.att_part, ATT ? a.att_part_bytes : 0);
+  if (ATT)
+    xs.load_att(a, rp);
+  else
+    xs.load(make_rsrc(a.x, a.in * 4), make_rsrc(a.norm_w, a.norm_w ? a.in * 4 : 0));
   __builtin_amdgcn_sched_barrier(0);  // keep the x loads ahead of the weight loads
 
   auto row_off = [&](uint32_t unit) -> uint32_t {
@@ -325,7 +392,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
     for (int r = 0; r < R; ++r) acc[r] = 0.f;
     if (gl == 0 && row < sg.rows) {
       if (MODE == GEMV_STORE) sg.out[row] = sg.bias ? acc0 + ex : acc0;  // model.rs:179-183
-      if (MODE == GEMV_RESID) {
+      if (RES) {
         float v = ex + acc0;  // tensor.rs:232
         sg.out[row] = v;
         if (sg.out2) sg.out2[row] = v;
@@ -351,6 +418,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   issue(iu, is, ra, ea);
   next(iu, is);
   __builtin_amdgcn_sched_barrier(0);
+  if (ATT) xs.merge_att(a, rp);
   xs.finish(a.in, a.norm_w != nullptr, a.eps, xf, pl, red4);
   for (uint32_t f = 0; f < n_steps; f += 2) {
     issue(iu, is, rb, eb);  // past the wave's last step: rows past the end, loads of zeros
@@ -381,7 +449,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
 // T0 serves every segment whose type is T0, T1 the others (T1 == T0 for
 // single-format launches), so each kernel carries one or two format paths.
 // NX: 8-value groups of x per thread (in <= 2048 * NX); NORM: rmsnorm
-// support (only the small-in kernels, where the norms occur).
+// support (only the small-in kernels, where the norms occur).  MODE
+// GEMV_RESID_ATT stages x from the attention partials (in <= 4096).
 template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX>
 __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
   constexpr bool NORM = NX <= 2;
@@ -467,6 +536,7 @@ static hipError_t go(GemvArgs a, hipStream_t s, uint32_t* nblocks) {
 // rmsnorm and only for STORE/RESID, in <= 20480 (the FFN down projection).
 template <uint32_t T0, uint32_t T1, int MODE, int LPR>
 static hipError_t pick_nx(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
+  if (a.in <= 2048) return go<T0, T1, LPR, MODE, 1>(a, s, nb);
   if (a.in <= 4096) return go<T0, T1, LPR, MODE, 2>(a, s, nb);
   if constexpr (MODE == GEMV_STORE || MODE == GEMV_RESID)
     if (a.norm_w == nullptr && a.in <= 20480) return go<T0, T1, LPR, MODE, 10>(a, s, nb);
@@ -528,18 +598,20 @@ hipError_t launch_gemv(GemvArgs a, GemvMode mode, hipStream_t s, uint32_t* nb) {
     case GEMV_RESID: return launch_split<GEMV_RESID>(a, s, nb);
     case GEMV_SWIGLU: return launch_split<GEMV_SWIGLU>(a, s, nb);
     case GEMV_ARGMAX: return launch_split<GEMV_ARGMAX>(a, s, nb);
+    case GEMV_RESID_ATT:
+      if (!a.att_part || !a.st || a.in % 8 || a.att_hd % 8 || (uint64_t)a.att_part_bytes >= BUF_INVALID)
+        return hipErrorInvalidValue;
+      return launch_split<GEMV_RESID_ATT>(a, s, nb);
   }
   return hipErrorInvalidValue;
 }
 
+// Only the in > 4096 kernels (NX = 10) use more than the default 64 KiB of
+// dynamic LDS.
 template <uint32_t T0, uint32_t T1, int LPR>
 static hipError_t prep_one(int bytes) {
   hipError_t e;
   const auto attr = hipFuncAttributeMaxDynamicSharedMemorySize;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 2>, attr, bytes))) return e;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 2>, attr, bytes))) return e;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_SWIGLU, 2>, attr, bytes))) return e;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_ARGMAX, 2>, attr, bytes))) return e;
   if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 10>, attr, bytes))) return e;
   return hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 10>, attr, bytes);
 }
@@ -587,25 +659,24 @@ hipError_t launch_embed(const uint8_t* table, uint32_t type, uint32_t hidden, ui
 //    FMA contraction, so q/k match the CPU bit for bit given equal inputs);
 //  - the block holding the step position appends head g's k/v to the cache;
 //  - scores, chunk softmax and P.V from K rows in registers and V rows in
-//    LDS, all loads issued up front; partial (o, m, l) per head to `part`;
-//  - the last block of kv head g to finish (atomic counter) merges the
-//    splits into att and re-zeroes the counter.
-template <int HD, int GQM>
+//    LDS; every global load of the block is issued before any is used;
+//  - writes its partial (o = sum_t e^(s_t - m) v_t, m, l = sum_t e^(s_t - m))
+//    per query head to `part`; the o-proj GEMV (GEMV_RESID_ATT) merges the
+//    splits while it stages its input, so no block waits on another here.
+template <int HD, int GQ>
 __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, const float* __restrict__ kn,
                                                    const float* __restrict__ vn, const float* __restrict__ cs,
                                                    float* __restrict__ kc, float* __restrict__ vc, uint32_t nh,
                                                    uint32_t nkv, uint32_t max_splits, float scale,
-                                                   float* __restrict__ part, uint32_t* counters,
-                                                   float* __restrict__ att, const StepState* st) {
-  constexpr int C = ATT_CHUNK, TPP = 256 / C, DPT = HD / TPP, PARTS = 256 / HD, HALF = HD / 2;
-  __shared__ float qs[GQM * HD];
+                                                   float* __restrict__ part, const StepState* st) {
+  constexpr int C = ATT_CHUNK, TPP = 256 / C, DPT = HD / TPP, PARTS = 256 / HD, HALF = HD / 2, NP = C / PARTS;
+  constexpr int RR = (GQ * HALF + HALF + 255) / 256;  // rotation rounds per thread
+  __shared__ __align__(16) float qs[GQ * HD];
   __shared__ float kcur[HD], vcur[HD];
-  __shared__ float vs[C * HD];
-  __shared__ float ps[GQM * C];
-  __shared__ float ml[GQM * 2];
-  __shared__ float osum[PARTS * GQM * HD];
-  __shared__ uint32_t last_flag;
-  const int GQ = (int)(nh / nkv);
+  __shared__ __align__(16) float vs[C * HD];
+  __shared__ __align__(16) float ps[GQ * C];
+  __shared__ float ml[GQ * 2];
+  __shared__ float osum[PARTS * GQ * HD];
   const uint32_t pos = st->pos, T = pos + 1, g = blockIdx.x, split = blockIdx.y, t0 = split * C;
   if (t0 >= T) return;
   const uint32_t n = min((uint32_t)C, T - t0), ns = (T + C - 1) / C;
@@ -621,18 +692,34 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     kr[i] = ((const float4*)(kc + off))[i];
     vr[i] = ((const float4*)(vc + off))[i];
   }
+  // rotation inputs: pair i < GQ*HALF of the query heads, then HALF of the key
   const float* cr = cs + (size_t)pos * HD;
-  for (int i = threadIdx.x; i < GQ * HALF + HALF; i += 256) {
-    int h = i / HALF, j = i % HALF;
+  float ra[RR], rb[RR], rc[RR], rs[RR];
+#pragma unroll
+  for (int r = 0; r < RR; ++r) {
+    int i = threadIdx.x + 256 * r;
+    if (i >= GQ * HALF + HALF) i = 0;  // clamped: loaded, not used
+    const int h = i / HALF, j = i % HALF;
     const float* src = h < GQ ? q + (size_t)(g * GQ + h) * HD : kn + (size_t)g * HD;
-    float a0 = src[j], b0 = src[j + HALF], c0 = cr[j], s0 = cr[HALF + j];
-    float r0 = __fsub_rn(__fmul_rn(a0, c0), __fmul_rn(b0, s0));
-    float r1 = __fadd_rn(__fmul_rn(a0, s0), __fmul_rn(b0, c0));
-    float* dst = h < GQ ? qs + h * HD : kcur;
-    dst[j] = r0;
-    dst[j + HALF] = r1;
+    ra[r] = src[j];
+    rb[r] = src[j + HALF];
+    rc[r] = cr[j];
+    rs[r] = cr[HALF + j];
   }
-  for (int d = threadIdx.x; d < HD; d += 256) vcur[d] = vn[(size_t)g * HD + d];
+  const float vnew = vn[(size_t)g * HD + (threadIdx.x % HD)];
+#pragma unroll
+  for (int r = 0; r < RR; ++r) {
+    const int i = threadIdx.x + 256 * r;
+    if (i < GQ * HALF + HALF) {
+      const int h = i / HALF, j = i % HALF;
+      float r0 = __fsub_rn(__fmul_rn(ra[r], rc[r]), __fmul_rn(rb[r], rs[r]));
+      float r1 = __fadd_rn(__fmul_rn(ra[r], rs[r]), __fmul_rn(rb[r], rc[r]));
+      float* dst = h < GQ ? qs + h * HD : kcur;
+      dst[j] = r0;
+      dst[j + HALF] = r1;
+    }
+  }
+  if (threadIdx.x < HD) vcur[threadIdx.x] = vnew;
   __syncthreads();
   if (split == ns - 1)  // KvCache::append of head g at pos
     for (int d = threadIdx.x; d < HD; d += 256) {
@@ -649,20 +736,26 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
 #pragma unroll
   for (int i = 0; i < DPT / 4; ++i)
     ((float4*)(vs + p * HD + sub * DPT))[i] = valid ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  {  // scores of position p for all GQ heads at once (independent accumulators)
+    float sc[GQ];
 #pragma unroll
-  for (int h = 0; h < GQM; ++h) {
-    if (h < GQ) {
-      const float4* qh = (const float4*)(qs + h * HD + sub * DPT);
-      float sdot = 0.f;
+    for (int h = 0; h < GQ; ++h) sc[h] = 0.f;
 #pragma unroll
-      for (int i = 0; i < DPT / 4; ++i) {
-        float4 a = kr[i], b = qh[i];
-        sdot += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+    for (int i = 0; i < DPT / 4; ++i) {
+      const float4 a = kr[i];
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) {
+        const float4 b = ((const float4*)(qs + h * HD + sub * DPT))[i];
+        sc[h] += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
       }
-#pragma unroll
-      for (int o = TPP / 2; o > 0; o >>= 1) sdot += __shfl_xor(sdot, o, TPP);
-      if (sub == 0) ps[h * C + p] = valid ? sdot * scale : -INFINITY;  // model.rs:397
     }
+#pragma unroll
+    for (int o = TPP / 2; o > 0; o >>= 1)
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) sc[h] += __shfl_xor(sc[h], o, TPP);
+    if (sub == 0)
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) ps[h * C + p] = valid ? sc[h] * scale : -INFINITY;  // model.rs:397
   }
   __syncthreads();
   const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -678,25 +771,32 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     }
   }
   __syncthreads();
+  // P.V: thread (d, prt) sums positions [NP prt, NP prt + NP) for all GQ
+  // heads; masked positions have p = 0 and zero V rows
   const int d = threadIdx.x % HD, prt = threadIdx.x / HD;
-  float acc[GQM];
+  {
+    float acc[GQ];
 #pragma unroll
-  for (int h = 0; h < GQM; ++h) acc[h] = 0.f;
-  for (uint32_t t = prt; t < n; t += PARTS) {
-    float vv = vs[t * HD + d];
+    for (int h = 0; h < GQ; ++h) acc[h] = 0.f;
 #pragma unroll
-    for (int h = 0; h < GQM; ++h)
-      if (h < GQ) acc[h] += ps[h * C + t] * vv;
+    for (int j = 0; j < NP; j += 4) {
+      const int t = prt * NP + j;
+      const float v0 = vs[t * HD + d], v1 = vs[(t + 1) * HD + d], v2 = vs[(t + 2) * HD + d], v3 = vs[(t + 3) * HD + d];
+#pragma unroll
+      for (int h = 0; h < GQ; ++h) {
+        const float4 pp = *(const float4*)(ps + h * C + t);
+        acc[h] += pp.x * v0 + pp.y * v1 + pp.z * v2 + pp.w * v3;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) osum[(prt * GQ + h) * HD + d] = acc[h];
   }
-#pragma unroll
-  for (int h = 0; h < GQM; ++h)
-    if (h < GQ) osum[(prt * GQM + h) * HD + d] = acc[h];
   __syncthreads();
   for (int i = threadIdx.x; i < GQ * HD; i += 256) {
     int h = i / HD, dd = i % HD;
     float o = 0.f;
 #pragma unroll
-    for (int pp = 0; pp < PARTS; ++pp) o += osum[(pp * GQM + h) * HD + dd];
+    for (int pp = 0; pp < PARTS; ++pp) o += osum[(pp * GQ + h) * HD + dd];
     float* dst = part + ((size_t)(g * GQ + h) * max_splits + split) * (HD + 2);
     dst[dd] = o;
     if (dd == 0) {
@@ -704,48 +804,46 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
       dst[HD + 1] = ml[2 * h + 1];
     }
   }
-  // publish the partial, count finished splits of kv head g
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last_flag = atomicAdd(&counters[g], 1u) == ns - 1;
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  if (threadIdx.x == 0) counters[g] = 0;
-  for (int i = threadIdx.x; i < GQ * HD; i += 256) {
-    int h = i / HD, dd = i % HD;
-    const float* P = part + (size_t)(g * GQ + h) * max_splits * (HD + 2);
-    float M = -INFINITY;
-    for (uint32_t sp = 0; sp < ns; ++sp) M = fmaxf(M, P[sp * (HD + 2) + HD]);
-    float L = 0.f, o = 0.f;
-    for (uint32_t sp = 0; sp < ns; ++sp) {
-      float w = expf(P[sp * (HD + 2) + HD] - M);
-      L += P[sp * (HD + 2) + HD + 1] * w;
-      o += P[sp * (HD + 2) + dd] * w;
-    }
-    att[(size_t)(g * GQ + h) * HD + dd] = o / L;
-  }
 }
 
 size_t attention_part_floats(uint32_t nh, uint32_t hd, uint32_t max_ctx) {
-  uint32_t ms = (max_ctx + ATT_CHUNK - 1) / ATT_CHUNK;
-  return (size_t)nh * ms * (hd + 2);
+  return (size_t)nh * attention_splits(max_ctx) * (hd + 2);
 }
+
+template <int HD, int GQ>
+static void att_go(dim3 grid, hipStream_t s, const float* q, const float* k, const float* v, const float* cs,
+                   float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms, float scale, float* part,
+                   const StepState* st) {
+  hipLaunchKernelGGL((k_attention<HD, GQ>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, scale, part, st);
+}
+
+template <int HD>
+static hipError_t att_gq(uint32_t gq, dim3 grid, hipStream_t s, const float* q, const float* k, const float* v,
+                         const float* cs, float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms, float scale,
+                         float* part, const StepState* st) {
+  switch (gq) {
+#define FRN_ATT_GQ(n) \
+  case n: att_go<HD, n>(grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, scale, part, st); break;
+    FRN_ATT_GQ(1) FRN_ATT_GQ(2) FRN_ATT_GQ(3) FRN_ATT_GQ(4) FRN_ATT_GQ(5) FRN_ATT_GQ(6) FRN_ATT_GQ(7) FRN_ATT_GQ(8)
+#undef FRN_ATT_GQ
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+bool attention_supported(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim) {
+  return n_kv_heads && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= 8 && (head_dim == 64 || head_dim == 128);
+}
+
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, const float* cs, float* kc, float* vc,
                             uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx, float scale, float* part,
-                            uint32_t* counters, float* att, const StepState* st, hipStream_t s) {
-  uint32_t ms = (max_ctx + ATT_CHUNK - 1) / ATT_CHUNK, gq = nh / nkv;
+                            const StepState* st, hipStream_t s) {
+  if (!attention_supported(nh, nkv, hd)) return hipErrorInvalidValue;
+  uint32_t ms = attention_splits(max_ctx), gq = nh / nkv;
   dim3 grid(nkv, ms);
-  if (hd == 128 && gq <= 8)
-    hipLaunchKernelGGL((k_attention<128, 8>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, scale, part,
-                       counters, att, st);
-  else if (hd == 64 && gq <= 16)
-    hipLaunchKernelGGL((k_attention<64, 16>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, scale, part,
-                       counters, att, st);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  if (hd == 128) return att_gq<128>(gq, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, scale, part, st);
+  return att_gq<64>(gq, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, scale, part, st);
 }
 
 // ---- step bookkeeping and argmax (generate.rs:69-77) ------------------------

@@ -16,7 +16,9 @@ struct StepState {
   uint32_t pad[5];
 };
 
-enum GemvMode : int { GEMV_STORE = 0, GEMV_RESID = 1, GEMV_SWIGLU = 2, GEMV_ARGMAX = 3 };
+// RESID_ATT: RESID whose x is the attention output, merged from the
+// attention kernel's per-split partials while staging.
+enum GemvMode : int { GEMV_STORE = 0, GEMV_RESID = 1, GEMV_SWIGLU = 2, GEMV_ARGMAX = 3, GEMV_RESID_ATT = 4 };
 
 // One weight matrix of a (possibly multi-matrix) GEMV launch.  All segments
 // of a launch share the input vector x and its optional rmsnorm.
@@ -38,6 +40,11 @@ struct GemvArgs {
   const float* norm_w;  // optional rmsnorm gain applied to x first (tensor.rs:164-185)
   float eps;
   uint64_t* best;       // ARGMAX: one packed (logit, ~row) candidate per block
+  // RESID_ATT: partials [n_heads][att_ms][att_hd + 2] = (o[att_hd], m, l) of
+  // splits of att_chunk positions; the number of splits follows st->pos
+  const float* att_part;
+  const StepState* st;
+  uint32_t att_ms, att_hd, att_chunk, att_part_bytes;
 };
 
 hipError_t launch_dequant(uint32_t type, const uint8_t* raw, size_t n_elems, float* out, hipStream_t s);
@@ -51,14 +58,18 @@ uint32_t gemv_blocks(uint32_t type, uint32_t rows, uint32_t in);
 
 hipError_t launch_embed(const uint8_t* table, uint32_t type, uint32_t hidden, uint32_t row_bytes, StepState* st,
                         float* x, hipStream_t s);
-// RoPE(q), RoPE(k) at the step's position, KV-cache append, split-sequence
-// GQA attention and the split combine, in one launch.  counters holds
-// n_kv_heads zeroed words (left zeroed on exit).
+// RoPE(q), RoPE(k) at the step's position, KV-cache append and
+// split-sequence GQA attention in one launch; writes the per-split partials
+// that a GEMV_RESID_ATT launch merges (layout in GemvArgs).
 hipError_t launch_attention(const float* q, const float* k, const float* v, const float* rope_cs, float* k_cache,
                             float* v_cache, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                            uint32_t max_ctx, float scale, float* part, uint32_t* counters, float* att,
-                            const StepState* st, hipStream_t s);
+                            uint32_t max_ctx, float scale, float* part, const StepState* st, hipStream_t s);
 size_t attention_part_floats(uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx);
+uint32_t attention_splits(uint32_t max_ctx);  // att_ms
+constexpr uint32_t ATTENTION_CHUNK = 64;      // att_chunk
+// Shapes the attention kernel handles: head_dim 64 or 128, at most 8 query
+// heads per kv head.
+bool attention_supported(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
 // Ends a step: reduces the lm_head kernel's per-block argmax candidates
 // (best == nullptr for a step without logits) and advances the position.
 hipError_t launch_step_end(StepState* st, const uint64_t* best, uint32_t n_best, hipStream_t s);
