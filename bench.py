@@ -98,7 +98,21 @@ def main():
     ap.add_argument("--gguf", default=None, help="use this GGUF instead of writing the synthetic one")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one (for profilers) instead of "
                     "replaying the captured decode graph")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device-to-device copy of BYTES, 5 times (calibrates the HBM byte "
+                         "counters of rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE against a known size), then exit")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
+                    help="measured HBM bytes per launch (from rocprofv3 --pmc runs) to report as roofline.traffic")
     args = ap.parse_args()
+    if args.copy_probe:
+        import torch
+        src = torch.empty(args.copy_probe // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied %d bytes 5 times" % args.copy_probe)
+        return
     if args.gpus != 1:
         print("bench.py: this engine runs on one GPU; --gpus %d is not supported (sharding is design-only)" %
               args.gpus, file=sys.stderr)
@@ -159,11 +173,42 @@ def main():
     for k, (ms, calls) in tm.items():
         if calls:
             log("  %-10s %9.3f ms  %6d calls  %8.2f us/call" % (k, ms, calls, 1000 * ms / calls))
-    # dominant kernel: the fused gate/up GEMV + SwiGLU (largest share of time)
-    gu_ms, gu_calls = tm["gate_up"]
-    gu_bytes = (sum(per["ffn_gate.weight"]) + sum(per["ffn_up.weight"])) / c.n_layers + 4 * (c.hidden + c.ffn)
-    gu_avg_s = gu_ms * 1e-3 / gu_calls
-    gu_gbs = gu_bytes / gu_avg_s / 1e9
+    # per-kernel algorithmic bytes and replayed launch durations.  Each
+    # category is replayed over every layer in turn (the weights then stream
+    # from HBM, as in a decode step), so the mean per launch carries no
+    # per-launch event overhead; rocprofv3's kernel trace of the same run
+    # gives the same means (profiles/).
+    L = c.n_layers
+    pos = model.cache_len()
+    ns = pos // 64 + 1
+    qd, kvd = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+    part_b = ns * c.n_heads * (c.head_dim + 2) * 4
+    avg = lambda names: sum(sum(per[n]) for n in names) / L
+    kbytes = {
+        "qkv": avg(["attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_q.bias", "attn_k.bias", "attn_v.bias",
+                    "attn_norm.weight"]) + 4 * (c.hidden + qd + 2 * kvd),
+        "attention": 2 * (pos + 1) * kvd * 4 + 4 * (qd + 2 * kvd) + part_b,
+        "o_proj": avg(["attn_output.weight"]) + part_b + 2 * 4 * c.hidden,
+        "gate_up": avg(["ffn_gate.weight", "ffn_up.weight", "ffn_norm.weight"]) + 4 * (c.hidden + c.ffn),
+        "down": avg(["ffn_down.weight"]) + 4 * (c.ffn + 2 * c.hidden),
+        "lm_head": lm_bytes + 4 * (2 * c.hidden + c.vocab),
+    }
+    per_step = {"qkv": L, "attention": L, "o_proj": L, "gate_up": L, "down": L, "lm_head": 1}
+    kern = {}
+    for k in kbytes:
+        us = model.bench_kernel(k, None, 2 if k == "lm_head" else 4)
+        kern[k] = {"avg_us": round(us, 3), "bytes": int(kbytes[k]), "gbs": round(kbytes[k] / us * 1e-3, 1),
+                   "us_per_step": round(us * per_step[k], 1)}
+        log("  replay %-10s %8.2f us/launch  %8.1f GB/s  %7.1f us/step" %
+            (k, us, kbytes[k] / us * 1e-3, us * per_step[k]))
+    model.reset()
+    dom = max(kern, key=lambda k: kern[k]["us_per_step"])
+    dk = kern[dom]
+    traffic = None
+    if os.path.exists(args.traffic):
+        with open(args.traffic) as f:
+            tr = json.load(f).get("bytes_per_launch", {})
+        traffic = tr.get("%s/%s" % (args.model, dom))
 
     cpu = None
     if not args.no_cpu:
@@ -190,10 +235,10 @@ def main():
                    "decode_tokens": args.steps, "bytes_per_token": int(step_bytes),
                    "hbm_frac_per_token": round(step_gbs / HBM_PEAK_GBS, 4),
                    "prefill_tokens_per_s": round(args.prompt / prefill_s, 1)},
-        "roofline": {"bound": "hbm", "kernel": "gate_up (fused Q4_K gate+up GEMV + SwiGLU)",
-                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": int(gu_bytes), "avg_us": round(gu_avg_s * 1e6, 3)},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": dk["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_per_launch": dk["bytes"], "avg_us": dk["avg_us"]},
+        "kernels": kern,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -74,6 +74,7 @@ SIGNATURES = {
     "frn_timings_enable": (_I, [_P, _I]),
     "frn_timings_reset": (_I, [_P]),
     "frn_timings": (_I, [_P, ctypes.POINTER(Timing), _U32, ctypes.POINTER(_U32)]),
+    "frn_bench_kernel": (_I, [_P, ctypes.c_char_p, _U32, _U32, ctypes.POINTER(ctypes.c_float)]),
     "frn_dequant": (_I, [_U32, _P, _SZ, _SZ, _P, _P]),
     "frn_matmul_quant": (_I, [_U32, _P, _SZ, _P, _U32, _P, _U32, _U32, _P]),
     "frn_argmax": (_I, [_P, _SZ, _P, _P]),
@@ -313,6 +314,15 @@ class Model:
         n = ctypes.c_uint32()
         check(load().frn_timings(self.ctx, arr, 32, ctypes.byref(n)))
         return {arr[i].name.decode(): (arr[i].ms, arr[i].calls) for i in range(n.value)}
+
+    def bench_kernel(self, name, layer=None, reps=10):
+        """Mean time per launch (us) of one kernel category replayed back to
+        back (layer None: every layer in turn, reps rounds); leaves the
+        context state undefined (reset() afterwards)."""
+        layer = 0xFFFFFFFF if layer is None else layer
+        us = ctypes.c_float()
+        check(load().frn_bench_kernel(self.ctx, name.encode(), layer, reps, ctypes.byref(us)))
+        return us.value
 
     def close(self):
         lib = load()

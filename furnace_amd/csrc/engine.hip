@@ -244,10 +244,22 @@ static frn_status need(frn_ctx* c, const std::string& name, uint64_t out, uint64
 }
 
 // Event pair around one kernel when the step runs eagerly for --timings.
+// Replay mode (rcat >= 0): launch only category rcat of layer rlayer (the
+// per-step kernels match any layer), reps times back to back.
 struct Tick {
   frn_ctx* c;
   bool on;
   size_t n = 0;
+  int rcat = -1, rlayer = -1, layer = -1;  // rlayer -1: every layer
+  uint32_t reps = 0, launched = 0;
+  template <class F>
+  hipError_t replay(int cat, F&& launch) {
+    if (cat != rcat || (layer >= 0 && rlayer >= 0 && layer != rlayer)) return hipSuccess;
+    ++launched;
+    for (uint32_t r = 0; r < reps; ++r)
+      if (hipError_t e = launch()) return e;
+    return hipSuccess;
+  }
   hipError_t begin(int cat) {
     if (!on) return hipSuccess;
     if (c->ev.size() < 2 * (n + 1)) {
@@ -277,7 +289,8 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
   hipStream_t s = c->stream;
   hipError_t e;
   float scale = 1.0f / sqrtf((float)g.head_dim);  // model.rs:384
-#define TIMED(cat, call) ((e = tk.begin(cat)) ? e : (e = tk.end(call)))
+#define TIMED(cat, call) \
+  (tk.rcat >= 0 ? (e = tk.replay(cat, [&]() { return (call); })) : ((e = tk.begin(cat)) ? e : (e = tk.end(call))))
   if (TIMED(CAT_EMBED, launch_embed(c->embd->ptr, c->embd->type, g.hidden,
                                     (uint32_t)type_row_bytes(c->embd->type, g.hidden), c->st, c->x, s)))
     return e;
@@ -305,6 +318,7 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
   const uint32_t H = g.hidden, QD = g.n_heads * g.head_dim;
   for (uint32_t l = 0; l < g.n_layers; ++l) {
     const LayerPtrs& L = c->layers[l];
+    tk.layer = (int)l;
     // rmsnorm + q/k/v GEMVs + biases in one launch (model.rs:456-459)
     GemvArgs qkv = args(H, c->x, L.attn_norm);
     qkv.n_seg = 3;
@@ -336,6 +350,7 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
     dn.seg[0] = seg(L.down, nullptr, nullptr, c->x, c->x);
     if (TIMED(CAT_DOWN, launch_gemv(dn, GEMV_RESID, s))) return e;
   }
+  tk.layer = -1;
   if (with_logits) {  // last_row_logits + argmax (model.rs:594-600, generate.rs:69-77)
     GemvArgs lm = args(H, c->x, c->out_norm);
     lm.seg[0] = seg(c->lm_head, nullptr, nullptr, c->logits, nullptr);
@@ -556,6 +571,38 @@ extern "C" frn_status frn_timings(frn_ctx* c, frn_timing* out, uint32_t max, uin
     ++k;
   }
   *n = k;
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_bench_kernel(frn_ctx* c, const char* name, uint32_t layer, uint32_t reps, float* avg_us) {
+  if (!c || !name || !avg_us || reps == 0) return fail(FRN_EINVAL, "frn_bench_kernel: bad argument");
+  int cat = -1;
+  for (int i = 0; i < N_CAT; ++i)
+    if (!strcmp(name, CAT_NAMES[i])) cat = i;
+  if (cat < 0) return fail(FRN_EINVAL, "frn_bench_kernel: no kernel category '%s'", name);
+  if (layer != FRN_ALL_LAYERS && layer >= c->cfg.n_layers)
+    return fail(FRN_EINVAL, "frn_bench_kernel: layer %u out of range", layer);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  hipEvent_t e0, e1;
+  HIP_TRY(hipEventCreate(&e0), "hipEventCreate");
+  if (hipError_t r = hipEventCreate(&e1)) {
+    (void)hipEventDestroy(e0);
+    return fail(FRN_EHIP, "hipEventCreate: %s", hipGetErrorString(r));
+  }
+  Tick tk{c, false};
+  tk.rcat = cat;
+  tk.rlayer = layer == FRN_ALL_LAYERS ? -1 : (int)layer;
+  tk.reps = layer == FRN_ALL_LAYERS ? 1 : reps;
+  hipError_t r = hipEventRecord(e0, c->stream);
+  for (uint32_t k = 0; !r && k < (layer == FRN_ALL_LAYERS ? reps : 1u); ++k) r = record_step(c, true, tk);
+  if (!r) r = hipEventRecord(e1, c->stream);
+  if (!r) r = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (!r) r = hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (r) return fail(FRN_EHIP, "frn_bench_kernel: %s", hipGetErrorString(r));
+  *avg_us = tk.launched ? ms * 1000.0f / (float)tk.launched : 0.f;
   return FRN_OK;
 }
 

@@ -306,6 +306,9 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
 }
 
 // ---- fused dequant-GEMV -----------------------------------------------------------
+#ifndef GEMV_MAX_GRID
+#define GEMV_MAX_GRID 512
+#endif
 // A block stages x (and applies the rmsnorm) once; then each of its 4 waves
 // works alone through "units" of G = 64 / LPR rows, one group of LPR lanes
 // per row (SWIGLU: per gate/up row pair).  Wave w of block b takes units
@@ -495,7 +498,13 @@ static int lanes_per_row(uint32_t total_rows, uint32_t type, int mode, int n_ite
   return best_l;
 }
 
-static uint32_t max_blocks(uint32_t in) { return gemv_lds_bytes(in, false) > 80 * 1024 ? 256 : 512; }
+// Grid cap: 2 blocks (8 waves) per CU for in <= 10240, 1 above.  (A cap
+// of 4 per CU, which LDS would allow for small in, measured no faster: the
+// kernels are VALU-bound, not short of waves.)
+static uint32_t max_blocks(uint32_t in) {
+  const size_t lds = gemv_lds_bytes(in, false);
+  return lds > 80 * 1024 ? 256 : lds > 40 * 1024 ? 512 : GEMV_MAX_GRID;
+}
 
 // Blocks per segment in proportion to its units of 64 / LPR rows; each
 // block runs 4 wave workers; at most as many blocks as are resident at once.

@@ -121,6 +121,18 @@ frn_status frn_timings_enable(frn_ctx* ctx, int enable);
 frn_status frn_timings_reset(frn_ctx* ctx);
 frn_status frn_timings(frn_ctx* ctx, frn_timing* out, uint32_t max, uint32_t* n);
 
+/* Measurement hook (no counterpart in the reference; used by the bench to
+ * price one kernel without per-launch event overhead): launches the kernel
+ * of timing category `name` (as in frn_timings) for `layer` `reps` times
+ * back to back on the context's stream, between one event pair, and
+ * returns the mean time per launch.  layer == FRN_ALL_LAYERS launches it
+ * for every layer in order, reps rounds, so the weights stream from HBM as
+ * in a decode step (one layer's weights replayed alone would stay in the
+ * 256 MB last-level cache).  Leaves the context's activations and position
+ * undefined: call frn_reset afterwards. */
+#define FRN_ALL_LAYERS 0xFFFFFFFFu
+frn_status frn_bench_kernel(frn_ctx* ctx, const char* name, uint32_t layer, uint32_t reps, float* avg_us);
+
 /* ---- single-op entry points (device pointers, caller's stream) ----------- */
 
 /* quant::dequantize (quant.rs:261-281) on device buffers: n_elems values of
