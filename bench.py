@@ -84,6 +84,43 @@ def cpu_baseline(path, prompt, budget_s, threads):
     return steps / dec, steps, dec, prefill_s
 
 
+GEMV_SHAPES = [("Q4_K", fa.Q4_K, 8960, 1536), ("Q4_K", fa.Q4_K, 1536, 8960), ("Q6_K", fa.Q6_K, 1536, 8960),
+               ("Q8_0", fa.Q8_0, 1536, 1536), ("Q6_K", fa.Q6_K, 151936, 1536)]
+
+
+def gemv_microbench(seed, reps=200):
+    """frn_matmul_quant at batch 1 on each shape: weights N(0, 0.02) quantized
+    by the synthetic-model encoders, x ~ N(0, 1).  The timed launches rotate
+    over copies of the weights totalling >= 512 MB, so they stream from HBM
+    rather than the 256 MB last-level cache.  Bytes = weights + x + y."""
+    hip = fa.Hip()
+    ev0, ev1 = hip.event(), hip.event()
+    for name, t, out, inn in GEMV_SHAPES:
+        w = fa.quantize(t, fa.gaussian(seed + out, 0.02, out * inn))
+        copies = max(1, min(64, -(-(512 << 20) // w.nbytes)))
+        wd = [hip.to_device(w) for _ in range(copies)]
+        xd = hip.to_device(fa.gaussian(seed + 1, 1.0, inn))
+        yd = hip.malloc(out * 4)
+        fa.matmul_quant_dev(t, wd[0], w.nbytes, xd, 1, yd, out, inn)
+        best = 1e30
+        for _ in range(3):
+            hip.record(ev0)
+            for i in range(reps):
+                fa.matmul_quant_dev(t, wd[i % copies], w.nbytes, xd, 1, yd, out, inn)
+            hip.record(ev1)
+            best = min(best, hip.elapsed_ms(ev0, ev1) * 1e3 / reps)
+        nbytes = w.nbytes + 4 * (inn + out)
+        gbs = nbytes / best * 1e-3
+        log("gemv %s [%d, %d]: %.2f us/launch, %.1f GB/s (%.1f%% of HBM peak), %d weight copies" %
+            (name, out, inn, best, gbs, 100 * gbs / HBM_PEAK_GBS, copies))
+        print(json.dumps({"metric": "fused dequant-GEMV bandwidth", "shape": "%s [%d, %d]" % (name, out, inn),
+                          "us_per_launch": round(best, 3), "bytes": nbytes, "value": round(gbs, 1),
+                          "unit": "GB/s", "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "batch": 1,
+                          "data": "synthetic N(0,0.02) weights, N(0,1) x"}), flush=True)
+        for p in wd + [xd, yd]:
+            hip.free(p)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,9 +138,15 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES, 5 times (calibrates the HBM byte "
                          "counters of rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE against a known size), then exit")
+    ap.add_argument("--gemv", action="store_true",
+                    help="instead of the decode loop, run the single-op fused dequant-GEMV microbench (batch 1, "
+                         "the five weight shapes of the decode step) and print one JSON line per shape")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="measured HBM bytes per launch (from rocprofv3 --pmc runs) to report as roofline.traffic")
     args = ap.parse_args()
+    if args.gemv:
+        gemv_microbench(args.seed)
+        return
     if args.copy_probe:
         import torch
         src = torch.empty(args.copy_probe // 4, dtype=torch.float32, device="cuda").fill_(1.0)
