@@ -107,7 +107,8 @@ __device__ __forceinline__ float decode_elem(uint32_t t, const uint8_t* b, int i
 //     plane 0..2: the chunk's digits d0, d1, d2 (signed bytes) with
 //                 x ~= s * (d0 + d1/128 + d2/16384) per 32-value chunk
 //                 (|error| <= max|x| * 2^-22 -- f32-level);
-//     plane 3:    {s / 16384, sum(x), sum(d0), 128*sum(d1) + sum(d2)}.
+//     plane 3:    {s / 16384, sum(x), -32*sum(d0), -32*(128*sum(d1) + sum(d2))}
+//                 (the digit sums pre-multiplied by Q6_K's -32 offset).
 // Records sit at chunk index swz(c), a permutation that spreads the chunks
 // a 16-lane group reads in one instruction over the LDS banks.
 // (Only whole groups of 8 chunks are permuted, so the map stays inside the
@@ -116,15 +117,40 @@ __device__ __forceinline__ uint32_t swz(uint32_t c, uint32_t n) {
   return c < (n & ~7u) ? c ^ (((c >> 3) & 1u) * 6u) : c;
 }
 
+// One staged 16-value chunk as the items use it: digit planes 0..2 and
+// the metadata record.
+struct XC {
+  uint4 a, b, d;
+  float4 m;
+};
+
+// The f32 form (every launch but the lm_head's): x itself and the sum of
+// each 16-value chunk, for the terms that multiply sum(x) (Q4_K's min,
+// Q6_K's -32 offset).  One chunk as the items use it:
+struct XF {
+  float4 v[4];
+  float s;
+};
+
 struct XLds {
   const float* xf;     // [K]
-  const uint8_t* pl;   // 4 planes of K bytes
+  const uint8_t* pl;   // int8 form: 4 planes of K bytes; f32 form: K/16 chunk sums
   uint32_t K;
-  __device__ __forceinline__ uint4 digits(uint32_t plane, uint32_t c) const {
-    return *(const uint4*)(pl + (size_t)plane * K + 16u * swz(c, K / 16));
+  __device__ __forceinline__ XF fchunk(uint32_t c) const {
+    XF x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x.v[i] = ((const float4*)xf)[4 * c + i];
+    x.s = ((const float*)pl)[c];
+    return x;
   }
-  __device__ __forceinline__ float4 meta(uint32_t c) const {
-    return *(const float4*)(pl + 3u * (size_t)K + 16u * swz(c, K / 16));
+  __device__ __forceinline__ XC chunk(uint32_t c) const {
+    const uint32_t o = 16u * swz(c, K / 16);
+    XC x;
+    x.a = *(const uint4*)(pl + o);
+    x.b = *(const uint4*)(pl + K + o);
+    x.d = *(const uint4*)(pl + 2u * K + o);
+    x.m = *(const float4*)(pl + 3u * K + o);
+    return x;
   }
 };
 
@@ -138,22 +164,26 @@ __device__ __forceinline__ int dot16(const uint32_t* q, uint4 d, int acc) {
 }
 // sum(q * x) over one 16-value chunk for small non-negative q (Q4_K: q < 16,
 // so 16 * 15 * 127 * 2^14 fits int32): one chain, scaled by the chunk scale.
-__device__ __forceinline__ float qx16_small(const uint32_t* q, const XLds& X, uint32_t c, float4& m) {
-  uint4 a = X.digits(0, c), b = X.digits(1, c), d = X.digits(2, c);
-  m = X.meta(c);
-  int acc = dot16(q, a, 0);
-  acc = dot16(q, b, acc << 7);
-  acc = dot16(q, d, acc << 7);
-  return (float)acc * m.x;
+__device__ __forceinline__ float qx16_small(const uint32_t* q, const XC& x) {
+  int acc = dot16(q, x.a, 0);
+  acc = dot16(q, x.b, acc << 7);
+  acc = dot16(q, x.d, acc << 7);
+  return (float)acc * x.m.x;
 }
-// sum((q - bias) * x) over one chunk for 8-bit q: the d0 part and the
-// d1/d2 part are accumulated separately so neither overflows int32.
-__device__ __forceinline__ float qx16_wide(const uint32_t* q, const XLds& X, uint32_t c, int bias) {
-  uint4 a = X.digits(0, c), b = X.digits(1, c), d = X.digits(2, c);
-  float4 m = X.meta(c);
-  int hi = dot16(q, a, 0) - bias * __float_as_int(m.z);
-  int lo = dot16(q, d, dot16(q, b, 0) << 7) - bias * __float_as_int(m.w);
-  return ((float)hi * 16384.0f + (float)lo) * m.x;
+// sum((q - 32) * x) over one chunk for Q6_K's 6-bit q (the offset enters
+// as the chunk's pre-multiplied digit sums, the accumulators' start
+// values); the d0 part and the d1/d2 part are accumulated separately so
+// neither overflows int32.
+__device__ __forceinline__ float qx16_q6(const uint32_t* q, const XC& x) {
+  int hi = dot16(q, x.a, __float_as_int(x.m.z));
+  int lo = dot16(q, x.d, (dot16(q, x.b, 0) << 7) + __float_as_int(x.m.w));
+  return ((float)hi * 16384.0f + (float)lo) * x.m.x;
+}
+// sum(q * x) over one chunk for signed 8-bit q (Q8_0).
+__device__ __forceinline__ float qx16_s8(const uint32_t* q, const XC& x) {
+  int hi = dot16(q, x.a, 0);
+  int lo = dot16(q, x.d, dot16(q, x.b, 0) << 7);
+  return ((float)hi * 16384.0f + (float)lo) * x.m.x;
 }
 
 // ---- GEMV items ---------------------------------------------------------
@@ -215,8 +245,13 @@ __device__ __forceinline__ Q4KRaw q4k_load(rsrc_t r, uint32_t row, int item) {
   o.q = bl128(r, sb + 16u + 16u * (item & 7));
   return o;
 }
-__device__ __forceinline__ float q4k_dot(const Q4KRaw& r, int item, const XLds& X) {
-  int k = item >> 3, j = item & 7, j64 = j >> 1, hh = j & 1;
+// staged chunks item `item` reads: low nibbles, high nibbles
+__device__ __forceinline__ uint32_t q4k_chunk(int item, int i) {
+  const int k = item >> 3, j = item & 7;
+  return 16u * k + 4u * (j >> 1) + (j & 1) + 2u * i;
+}
+__device__ __forceinline__ float q4k_dot(const Q4KRaw& r, int item, const XC& xA, const XC& xB) {
+  int j = item & 7, j64 = j >> 1;
   float d = f16_bits_to_f32(r.hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(r.hdr.x >> 16);
   uint32_t scA, mA, scB, mB;  // scales[12] live in hdr.y..hdr.w
   q4k_scale_min_regs(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j64, scA, mA);
@@ -224,10 +259,46 @@ __device__ __forceinline__ float q4k_dot(const Q4KRaw& r, int item, const XLds& 
   uint32_t lo[4] = {r.q.x & 0x0F0F0F0Fu, r.q.y & 0x0F0F0F0Fu, r.q.z & 0x0F0F0F0Fu, r.q.w & 0x0F0F0F0Fu};
   uint32_t hi[4] = {(r.q.x >> 4) & 0x0F0F0F0Fu, (r.q.y >> 4) & 0x0F0F0F0Fu, (r.q.z >> 4) & 0x0F0F0F0Fu,
                     (r.q.w >> 4) & 0x0F0F0F0Fu};
-  uint32_t cA = 16 * k + 4 * j64 + hh, cB = cA + 2;
-  float4 mtA, mtB;
-  float fA = qx16_small(lo, X, cA, mtA), fB = qx16_small(hi, X, cB, mtB);
-  return (d * (float)scA) * fA - (dmin * (float)mA) * mtA.y + (d * (float)scB) * fB - (dmin * (float)mB) * mtB.y;
+  float fA = qx16_small(lo, xA), fB = qx16_small(hi, xB);
+  return (d * (float)scA) * fA - (dmin * (float)mA) * xA.m.y + (d * (float)scB) * fB - (dmin * (float)mB) * xB.m.y;
+}
+
+// sum over 16 bytes w (4 dwords, byte i of w[k] is value 4k + i) of
+// byte * x (v_cvt_f32_ubyte{i} + FMA)
+__device__ __forceinline__ float bx16(const uint32_t* w, const XF& x) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    s = fmaf(byte_f(w[k], 0), x.v[k].x, s);
+    s = fmaf(byte_f(w[k], 1), x.v[k].y, s);
+    s = fmaf(byte_f(w[k], 2), x.v[k].z, s);
+    s = fmaf(byte_f(w[k], 3), x.v[k].w, s);
+  }
+  return s;
+}
+// the same for signed bytes (exact int8 -> f32)
+__device__ __forceinline__ float sx16(const uint32_t* w, const XF& x) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    s = fmaf((float)(int8_t)(w[k] & 0xFFu), x.v[k].x, s);
+    s = fmaf((float)(int8_t)((w[k] >> 8) & 0xFFu), x.v[k].y, s);
+    s = fmaf((float)(int8_t)((w[k] >> 16) & 0xFFu), x.v[k].z, s);
+    s = fmaf((float)(int8_t)(w[k] >> 24), x.v[k].w, s);
+  }
+  return s;
+}
+__device__ __forceinline__ float q4k_dot(const Q4KRaw& r, int item, const XF& xA, const XF& xB) {
+  int j = item & 7, j64 = j >> 1;
+  float d = f16_bits_to_f32(r.hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(r.hdr.x >> 16);
+  uint32_t scA, mA, scB, mB;
+  q4k_scale_min_regs(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j64, scA, mA);
+  q4k_scale_min_regs(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j64 + 1, scB, mB);
+  uint32_t lo[4] = {r.q.x & 0x0F0F0F0Fu, r.q.y & 0x0F0F0F0Fu, r.q.z & 0x0F0F0F0Fu, r.q.w & 0x0F0F0F0Fu};
+  uint32_t hi[4] = {(r.q.x >> 4) & 0x0F0F0F0Fu, (r.q.y >> 4) & 0x0F0F0F0Fu, (r.q.z >> 4) & 0x0F0F0F0Fu,
+                    (r.q.w >> 4) & 0x0F0F0F0Fu};
+  const float fA = bx16(lo, xA), fB = bx16(hi, xB);
+  return (d * (float)scA) * fA - (dmin * (float)mA) * xA.s + (d * (float)scB) * fB - (dmin * (float)mB) * xB.s;
 }
 
 // Q6_K: 8 items per superblock.  Item (k, h, lq, p): half h, value lanes
@@ -257,24 +328,45 @@ __device__ __forceinline__ Q6KRaw q6k_load(rsrc_t r, uint32_t row, int item) {
   o.d = bl16(r, sb + 208u);
   return o;
 }
-__device__ __forceinline__ float q6k_dot(const Q6KRaw& o, uint32_t row, int item, const XLds& X) {
+// staged chunks item `item` reads: quarter p, quarter p + 2
+__device__ __forceinline__ uint32_t q6k_chunk(int item, int i) {
+  const int k = item >> 3, rr = item & 7, h = rr >> 2, lq = (rr >> 1) & 1, p = rr & 1;
+  return 16u * k + 8u * h + 2u * p + lq + 4u * i;
+}
+// The item's 32 6-bit values as bytes (quarter p in v0, p + 2 in v1) and
+// its scale factors d*sc.
+__device__ __forceinline__ void q6k_unpack(const Q6KRaw& o, uint32_t row, int item, uint32_t (&v0)[4],
+                                           uint32_t (&v1)[4], float& ds0, float& ds1) {
   int k = item >> 3, rr = item & 7, h = rr >> 2, lq = (rr >> 1) & 1, p = rr & 1;
   const uint32_t sb = row + (uint32_t)k * 210u, sh = sb & 3u;
   const uint32_t ss = 8u * ((sb + 192u + 8u * h + 2u * p + lq) & 3u);
   float d = f16_bits_to_f32(o.d & 0xFFFFu);
-  float s0 = (float)(int8_t)((o.sc.x >> ss) & 0xFFu), s1 = (float)(int8_t)((o.sc.y >> ss) & 0xFFu);
+  ds0 = d * (float)(int8_t)((o.sc.x >> ss) & 0xFFu);
+  ds1 = d * (float)(int8_t)((o.sc.y >> ss) & 0xFFu);
   uint32_t lw[4], hw[4];
   realign16(o.ql, o.qlx, sh, lw);
   realign16(o.qh, o.qhx, sh, hw);
-  uint32_t v0[4], v1[4];
-  const uint32_t sh0 = 2 * p, sh1 = 2 * p + 4;
+  // nibble | 2 high bits << 4: a bit-field insert of the nibbles into the
+  // shifted high bits, then the top 2 bits cleared
+  const uint32_t sh0 = 2 * p;
+  constexpr uint32_t NIB = 0x0F0F0F0Fu;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {  // 6-bit values as bytes: nibble | 2 high bits << 4
-    v0[w] = (lw[w] & 0x0F0F0F0Fu) | (((hw[w] >> sh0) & 0x03030303u) << 4);
-    v1[w] = ((lw[w] >> 4) & 0x0F0F0F0Fu) | (((hw[w] >> sh1) & 0x03030303u) << 4);
+  for (int w = 0; w < 4; ++w) {
+    v0[w] = ((lw[w] & NIB) | ((hw[w] << (4 - sh0)) & ~NIB)) & 0x3F3F3F3Fu;
+    v1[w] = (((lw[w] >> 4) & NIB) | ((hw[w] >> sh0) & ~NIB)) & 0x3F3F3F3Fu;
   }
-  uint32_t c0 = 16 * k + 8 * h + 2 * p + lq, c1 = c0 + 4;
-  return (d * s0) * qx16_wide(v0, X, c0, 32) + (d * s1) * qx16_wide(v1, X, c1, 32);
+}
+__device__ __forceinline__ float q6k_dot(const Q6KRaw& o, uint32_t row, int item, const XC& x0, const XC& x1) {
+  uint32_t v0[4], v1[4];
+  float ds0, ds1;
+  q6k_unpack(o, row, item, v0, v1, ds0, ds1);
+  return ds0 * qx16_q6(v0, x0) + ds1 * qx16_q6(v1, x1);
+}
+__device__ __forceinline__ float q6k_dot(const Q6KRaw& o, uint32_t row, int item, const XF& x0, const XF& x1) {
+  uint32_t v0[4], v1[4];
+  float ds0, ds1;
+  q6k_unpack(o, row, item, v0, v1, ds0, ds1);
+  return ds0 * fmaf(-32.0f, x0.s, bx16(v0, x0)) + ds1 * fmaf(-32.0f, x1.s, bx16(v1, x1));  // (q - 32) . x
 }
 
 // Q8_0, rows with an even number of blocks: item = block pair (68 B,
@@ -293,16 +385,27 @@ __device__ __forceinline__ Q8PairRaw q8_0_pair_load(rsrc_t r, uint32_t row, int 
   v.f = bl32(r, o + 64u);
   return v;
 }
-__device__ __forceinline__ float q8_0_pair_dot(const Q8PairRaw& r, int item, const XLds& X) {
+__device__ __forceinline__ uint32_t q8_0_pair_chunk(int item, int i) { return 4u * item + i; }
+__device__ __forceinline__ float q8_0_pair_dot(const Q8PairRaw& r, const XC (&x)[4]) {
   const uint32_t v[17] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c.x,
                           r.c.y, r.c.z, r.c.w, r.e.x, r.e.y, r.e.z, r.e.w, r.f};
   float d0 = f16_bits_to_f32(v[0] & 0xFFFFu), d1 = f16_bits_to_f32(v[8] >> 16);
   uint32_t q0[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) q0[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], 2);  // bytes 2..34
-  uint32_t c = 4 * item;
-  float b0 = qx16_wide(q0, X, c, 0) + qx16_wide(q0 + 4, X, c + 1, 0);
-  float b1 = qx16_wide(v + 9, X, c + 2, 0) + qx16_wide(v + 13, X, c + 3, 0);  // bytes 36..68
+  float b0 = qx16_s8(q0, x[0]) + qx16_s8(q0 + 4, x[1]);
+  float b1 = qx16_s8(v + 9, x[2]) + qx16_s8(v + 13, x[3]);  // bytes 36..68
+  return d0 * b0 + d1 * b1;
+}
+__device__ __forceinline__ float q8_0_pair_dot(const Q8PairRaw& r, const XF (&x)[4]) {
+  const uint32_t v[17] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c.x,
+                          r.c.y, r.c.z, r.c.w, r.e.x, r.e.y, r.e.z, r.e.w, r.f};
+  float d0 = f16_bits_to_f32(v[0] & 0xFFFFu), d1 = f16_bits_to_f32(v[8] >> 16);
+  uint32_t q0[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q0[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], 2);
+  float b0 = sx16(q0, x[0]) + sx16(q0 + 4, x[1]);
+  float b1 = sx16(v + 9, x[2]) + sx16(v + 13, x[3]);
   return d0 * b0 + d1 * b1;
 }
 

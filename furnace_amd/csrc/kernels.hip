@@ -3,6 +3,8 @@
 #include "formats.hpp"
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace frn {
 
 constexpr int ATT_CHUNK = ATTENTION_CHUNK;  // positions per attention block (one wave per softmax row)
@@ -66,48 +68,65 @@ __host__ __device__ constexpr int gemv_bi(uint32_t t, int mode) {
   return (t == T_Q4_K || t == T_Q6_K ? 3 : 2) - (mode == GEMV_SWIGLU ? 1 : 0);
 }
 
-// Per-format raw-register type.  dot() gets the row's byte offset (alignment of the
-// 2-byte aligned formats) and its pointer (nullptr for a masked item; only
-// the odd-block fallback reads through it).
+// Per-format raw-register type, the NC staged chunks an item reads
+// (chunk(it, i)), and dot(), which gets the row's byte offset (alignment of
+// the 2-byte aligned formats), its pointer (nullptr for a masked item; only
+// the odd-block fallback reads through it) and the item's chunks.  NC == 0:
+// the item reads the f32 copy of x in LDS instead.
 template <uint32_t T>
 struct Fmt;
 template <>
 struct Fmt<T_Q4_K> {
   using Raw = Q4KRaw;
+  static constexpr int NC = 2;
+  static __device__ __forceinline__ uint32_t chunk(int it, int i, bool) { return q4k_chunk(it, i); }
   static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool) { return q4k_load(r, row, it); }
-  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t*, int it, const XLds& X, bool) {
-    return q4k_dot(w, it, X);
+  template <class XT>
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t*, int it, const XT* x,
+                                              const XLds&, bool) {
+    return q4k_dot(w, it, x[0], x[1]);
   }
 };
 template <>
 struct Fmt<T_Q6_K> {
   using Raw = Q6KRaw;
+  static constexpr int NC = 2;
+  static __device__ __forceinline__ uint32_t chunk(int it, int i, bool) { return q6k_chunk(it, i); }
   static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool) { return q6k_load(r, row, it); }
-  static __device__ __forceinline__ float dot(const Raw& w, uint32_t row, const uint8_t*, int it, const XLds& X,
-                                              bool) {
-    return q6k_dot(w, row, it, X);
+  template <class XT>
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t row, const uint8_t*, int it, const XT* x,
+                                              const XLds&, bool) {
+    return q6k_dot(w, row, it, x[0], x[1]);
   }
 };
 template <>
 struct Fmt<T_Q8_0> {
   using Raw = Q8PairRaw;
+  static constexpr int NC = 4;
+  static __device__ __forceinline__ uint32_t chunk(int it, int i, bool pairs) {
+    return pairs ? q8_0_pair_chunk(it, i) : 0u;
+  }
   static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool pairs) {
     return q8_0_pair_load(r, pairs ? row : BUF_INVALID, it);
   }
-  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t* rowp, int it, const XLds& X,
-                                              bool pairs) {
-    if (pairs) return q8_0_pair_dot(w, it, X);
+  template <class XT>
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t* rowp, int it, const XT* x,
+                                              const XLds& X, bool pairs) {
+    if (pairs) return q8_0_pair_dot(w, {x[0], x[1], x[2], x[3]});
     return rowp ? small_block_item(T_Q8_0, rowp, it, X.xf) : 0.f;
   }
 };
 template <>
 struct Fmt<T_Q5_0> {
   using Raw = Q5PairRaw;
+  static constexpr int NC = 0;
+  static __device__ __forceinline__ uint32_t chunk(int, int, bool) { return 0u; }
   static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool pairs) {
     return q5_0_pair_load(r, pairs ? row : BUF_INVALID, it);
   }
-  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t* rowp, int it, const XLds& X,
-                                              bool pairs) {
+  template <class XT>
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t* rowp, int it, const XT*,
+                                              const XLds& X, bool pairs) {
     if (pairs) return q5_0_pair_dot(w, it, X.xf);
     return rowp ? small_block_item(T_Q5_0, rowp, it, X.xf) : 0.f;
   }
@@ -118,13 +137,17 @@ struct F32Raw {
 template <>
 struct Fmt<T_F32> {  // 16 floats per item
   using Raw = F32Raw;
+  static constexpr int NC = 0;
+  static __device__ __forceinline__ uint32_t chunk(int, int, bool) { return 0u; }
   static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool) {
     Raw o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) o.w[i] = bl128(r, row + 64u * (uint32_t)it + 16u * i);
     return o;
   }
-  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t*, int it, const XLds& X, bool) {
+  template <class XT>
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t*, int it, const XT*,
+                                              const XLds& X, bool) {
     const float4* Xp = (const float4*)X.xf + it * 4;
     float s = 0.f;
 #pragma unroll
@@ -144,7 +167,7 @@ struct Fmt<T_F32> {  // 16 floats per item
 __device__ __forceinline__ float4 u4f(uint4 v) {
   return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
 }
-template <int NX, bool NORM, bool ATT>
+template <int NX, bool NORM, bool ATT, bool DIG>
 struct XStage {
   // ATT: x is the attention output, merged here from the per-split partials
   // (o, m, l) of the attention kernel: NB splits are loaded up front with
@@ -220,10 +243,11 @@ struct XStage {
     }
   }
   // rmsnorm (tensor.rs:164-185: x * (1 / sqrt(mean(x^2) + eps)) * w) when
-  // norm, then split every 32-value chunk into the int8 digit planes and
-  // metadata the quantized items read (XLds in formats.hpp) and keep the
-  // f32 values for the f32 items.  The 4 threads of a chunk are adjacent
-  // lanes; groups past K were loaded as zeros and are not stored.
+  // norm; then the f32 values and, in the f32 form (!DIG), the sum of every
+  // 16-value chunk, or, in the int8 form (DIG), every 32-value chunk split
+  // into the digit planes and metadata (XLds in formats.hpp).  The threads
+  // of a chunk are adjacent lanes; groups past K were loaded as zeros and
+  // are not stored.
   __device__ __forceinline__ void finish(uint32_t K, bool norm, float eps, float* xf, uint8_t* pl, float* red4) {
     float inv = 1.0f;
     if (NORM && norm) {
@@ -251,6 +275,12 @@ struct XStage {
       if (live) {
         ((float4*)xf)[2 * u] = a;
         ((float4*)xf)[2 * u + 1] = b;
+      }
+      if (!DIG) {
+        float s16 = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+        s16 += __shfl_xor(s16, 1, 2);
+        if (live && (u & 1) == 0) ((float*)pl)[u >> 1] = s16;
+        continue;
       }
       const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
       float amax = 0.f, xsum = 0.f;
@@ -291,7 +321,7 @@ struct XStage {
         *(uint2*)(pl + 2 * K + off) = make_uint2(w2[0], w2[1]);
         if ((u & 1) == 0)
           *(float4*)(pl + 3 * K + 16u * swz(c, n16)) =
-              make_float4(cs, xsum, __int_as_float(s0), __int_as_float(128 * s1 + s2));
+              make_float4(cs, xsum, __int_as_float(-32 * s0), __int_as_float(-32 * (128 * s1 + s2)));
       }
     }
     __syncthreads();
@@ -326,6 +356,15 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   constexpr bool ATT = MODE == GEMV_RESID_ATT;  // x = merged attention partials, then as RESID
   constexpr bool RES = MODE == GEMV_RESID || ATT;
   constexpr bool EX = MODE == GEMV_STORE || RES;  // per-row bias / residual input
+  constexpr int NCX = F::NC > 0 ? F::NC : 1;
+  constexpr bool PRELOAD = F::NC > 0 && F::NC <= 2;  // register budget: 16-17 VGPRs per chunk
+  // x as int8 digits (cheaper dot) for in <= 4096; the f32 form (far
+  // cheaper staging: no digits) for the long in of the FFN down projection,
+  // where each block would otherwise split 8960+ values into digits.
+  // Measured per launch (1.5B): down 11.6 -> 9.8 us with the f32 form;
+  // gate_up 9.9 vs 11.3 and o_proj 6.2 vs 6.7 us in favour of the digits.
+  constexpr bool DIG = NX <= 2;
+  using XT = typename std::conditional<DIG, XC, XF>::type;
   // the wave index through readfirstlane: the compiler then knows every
   // per-wave quantity below is uniform (scalar loop control, no exec masks)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -341,7 +380,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   const rsrc_t rex = make_rsrc(exp_, exp_ ? sg.rows * 4 : 0);
   const XLds X{xf, pl, a.in};
 
-  XStage<NX, NORM, ATT> xs;
+  XStage<NX, NORM, ATT, DIG> xs;
   const rsrc_t rp = make_rsrc(a.att_part, ATT ? a.att_part_bytes : 0);
   if (ATT)
     xs.load_att(a, rp);
@@ -371,17 +410,20 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
   uint64_t best = 0;
-  auto consume = [&](uint32_t unit, uint32_t step, Raw(&raw)[B], float ex) {
+  // xget(j, itc, xc): the staged chunks of the lane's j-th item of the step
+  auto consume = [&](uint32_t unit, uint32_t step, Raw(&raw)[B], float ex, auto&& xget) {
     const uint32_t row = unit * G + g, ro = row_off(unit);
 #pragma unroll
     for (int j = 0; j < BI; ++j) {
       const int it = (int)(step * BI + j) * LPR + gl;
       const bool ok = it < n_items && ro != BUF_INVALID;
       const int itc = ok ? it : 0;  // masked items read chunk 0 of x and have zero weights
+      XT xc[NCX];
+      xget(j, itc, xc);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const uint8_t* rp = ok ? (r == 0 ? sg.w : sg.w2) + ro : nullptr;
-        acc[r] += F::dot(raw[j * R + r], ro, rp, itc, X, pr);
+        acc[r] += F::dot(raw[j * R + r], ro, rp, itc, xc, X, pr);
       }
     }
     if (step + 1 < S) return;
@@ -408,6 +450,15 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
       }
     }
   };
+  auto from_lds = [&](int, int itc, XT* xc) {
+#pragma unroll
+    for (int i = 0; i < F::NC; ++i) {
+      if constexpr (DIG)
+        xc[i] = X.chunk(F::chunk(itc, i, pr));
+      else
+        xc[i] = X.fchunk(F::chunk(itc, i, pr));
+    }
+  };
 
   Raw ra[B], rb[B];
   float ea = 0.f, eb = 0.f;
@@ -418,21 +469,39 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
       u += stride;
     }
   };
+  auto run = [&](auto&& xget) {
+    for (uint32_t f = 0; f < n_steps; f += 2) {
+      issue(iu, is, rb, eb);  // past the wave's last step: rows past the end, loads of zeros
+      next(iu, is);
+      consume(cu, cs, ra, ea, xget);
+      next(cu, cs);
+      if (f + 1 >= n_steps) break;
+      issue(iu, is, ra, ea);
+      next(iu, is);
+      consume(cu, cs, rb, eb, xget);
+      next(cu, cs);
+    }
+  };
   issue(iu, is, ra, ea);
   next(iu, is);
   __builtin_amdgcn_sched_barrier(0);
   if (ATT) xs.merge_att(a, rp);
   xs.finish(a.in, a.norm_w != nullptr, a.eps, xf, pl, red4);
-  for (uint32_t f = 0; f < n_steps; f += 2) {
-    issue(iu, is, rb, eb);  // past the wave's last step: rows past the end, loads of zeros
-    next(iu, is);
-    consume(cu, cs, ra, ea);
-    next(cu, cs);
-    if (f + 1 >= n_steps) break;
-    issue(iu, is, ra, ea);
-    next(iu, is);
-    consume(cu, cs, rb, eb);
-    next(cu, cs);
+  if (PRELOAD && S == 1) {
+    // one step per unit: the lane reads the same items of every row it
+    // visits, so their staged chunks are read from LDS once, into registers
+    XT xr[BI][NCX];
+#pragma unroll
+    for (int j = 0; j < BI; ++j) {
+      const int it = j * LPR + gl;
+      from_lds(j, it < n_items ? it : 0, xr[j]);
+    }
+    run([&](int j, int, XT* xc) {
+#pragma unroll
+      for (int i = 0; i < F::NC; ++i) xc[i] = xr[j][i];
+    });
+  } else {
+    run(from_lds);
   }
   if (MODE == GEMV_ARGMAX) {
     for (int o = 32; o > 0; o >>= 1) {
@@ -474,7 +543,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
     gemv_body<T1, LPR, MODE, NX, NORM>(a, sg, blk, nblk, xf, pl, red4, best_s);
 }
 
-size_t gemv_lds_bytes(uint32_t in, bool) { return (size_t)in * 8; }
+// LDS of a launch: x as f32, then the int8 form's 4 planes of `in` bytes
+// (in <= 4096) or the f32 form's in/16 chunk sums.
+size_t gemv_lds_bytes(uint32_t in, bool) { return (size_t)in * (in <= 4096 ? 8 : 4) + in / 4; }
 
 
 // Lanes per row: the choice in {16, 32, 64} that keeps the most lanes busy
