@@ -76,6 +76,11 @@ struct frn_ctx {
   uint32_t n_best = 0;
   StepState* st = nullptr;
   StepState* h_st = nullptr;  // pinned mirror for read-back
+  // prefill rows: blocks of up to pf_rows prompt tokens through all layers
+  uint32_t pf_rows = 0;
+  float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_att = nullptr, *pf_act = nullptr,
+        *pf_inv = nullptr;
+  uint32_t* pf_ids = nullptr;
   uint32_t len = 0;           // host view of KvCache::len
   uint32_t last_next = 0xFFFFFFFFu;
   bool finalized = false, have_logits = false;
@@ -97,7 +102,7 @@ static void free_ctx(frn_ctx* c) {
   if (c->graph_prefill) (void)hipGraphDestroy(c->graph_prefill);
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -108,6 +113,23 @@ static void free_ctx(frn_ctx* c) {
 template <typename T>
 static hipError_t dmalloc(T** p, size_t bytes) {
   return hipMalloc((void**)p, bytes ? bytes : 16);
+}
+
+// Prefill works on blocks of up to PREFILL_ROWS tokens (64-row GEMM tiles).
+constexpr uint32_t PREFILL_ROWS = 256;
+
+static hipError_t alloc_prefill(frn_ctx* x) {
+  const frn_config& c = x->cfg;
+  const size_t P = std::min(c.max_ctx, PREFILL_ROWS), qd = (size_t)c.n_heads * c.head_dim,
+               kvd = (size_t)c.n_kv_heads * c.head_dim;
+  x->pf_rows = (uint32_t)P;
+  hipError_t e;
+  if ((e = dmalloc(&x->pf_x, P * c.hidden * 4)) || (e = dmalloc(&x->pf_q, P * qd * 4)) ||
+      (e = dmalloc(&x->pf_k, P * kvd * 4)) || (e = dmalloc(&x->pf_v, P * kvd * 4)) ||
+      (e = dmalloc(&x->pf_att, P * qd * 4)) || (e = dmalloc(&x->pf_act, P * c.ffn * 4)) ||
+      (e = dmalloc(&x->pf_inv, P * 4)) || (e = dmalloc(&x->pf_ids, P * 4)))
+    return e;
+  return hipSuccess;
 }
 
 extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** out) {
@@ -148,6 +170,7 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
       (e = dmalloc(&x->kcache, kv_bytes)) || (e = dmalloc(&x->vcache, kv_bytes)) ||
       (e = dmalloc(&x->rope, (size_t)c.max_ctx * c.head_dim * 4)) || (e = dmalloc(&x->st, sizeof(StepState))) ||
       (e = dmalloc(&x->best_part, ((size_t)c.vocab + 3) / 4 * 8)) ||  // >= lm_head blocks (4+ rows each)
+      (e = alloc_prefill(x)) ||
       (e = hipHostMalloc((void**)&x->h_st, sizeof(StepState), hipHostMallocDefault))) {
     free_ctx(x);
     return hip_fail(e, "frn_create: allocation");
@@ -483,6 +506,79 @@ static frn_status read_next(frn_ctx* c, uint32_t* next_id) {
   return FRN_OK;
 }
 
+// The prompt as blocks of rows (forward_cached with seq > 1, model.rs:579-592):
+// each block goes through every layer -- rmsnorm + q/k/v GEMMs (MFMA), RoPE
+// + KV append, causal attention over the cache, o-proj + residual, rmsnorm +
+// gate/up + SwiGLU, down + residual -- then the last row of the last block
+// gets the final norm, the lm_head GEMV and the argmax.
+static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
+  const frn_config& g = c->cfg;
+  hipStream_t s = c->stream;
+  hipError_t e;
+  const uint32_t H = g.hidden, QD = g.n_heads * g.head_dim, KVD = g.n_kv_heads * g.head_dim;
+  const float scale = 1.0f / sqrtf((float)g.head_dim);  // model.rs:384
+  uint32_t m = 0;
+  for (uint32_t c0 = 0; c0 < n; c0 += c->pf_rows) {
+    m = std::min(c->pf_rows, n - c0);
+    const uint32_t pos0 = c->len + c0;
+    if ((e = hipMemcpyAsync(c->pf_ids, ids + c0, (size_t)m * 4, hipMemcpyHostToDevice, s))) return e;
+    if ((e = launch_embed_rows(c->embd->ptr, c->embd->type, H, (uint32_t)type_row_bytes(c->embd->type, H), c->pf_ids,
+                               m, c->pf_x, s)))
+      return e;
+    auto gemm = [&](const DevTensor* w, const DevTensor* w2, const float* a, uint32_t K, const float* norm,
+                    const float* bias, float* out, uint32_t ldo, GemmMode mode) {
+      GemmArgs ga{};
+      ga.a = a;
+      ga.inv = norm ? c->pf_inv : nullptr;
+      ga.nw = norm;
+      ga.w = w->ptr;
+      ga.w2 = w2 ? w2->ptr : nullptr;
+      ga.type = w->type;
+      ga.row_bytes = (uint32_t)type_row_bytes(w->type, w->in);
+      ga.bias = bias;
+      ga.out = out;
+      ga.ldo = ldo;
+      ga.P = m;
+      ga.N = (uint32_t)w->out;
+      ga.K = K;
+      return launch_gemm(ga, mode, s);
+    };
+    for (uint32_t l = 0; l < g.n_layers; ++l) {
+      const LayerPtrs& L = c->layers[l];
+      const size_t lo = (size_t)l * g.max_ctx * KVD;
+      if ((e = launch_row_inv(c->pf_x, m, H, g.rms_eps, c->pf_inv, s)) ||
+          (e = gemm(L.wq, nullptr, c->pf_x, H, L.attn_norm, L.bq, c->pf_q, QD, GEMM_STORE)) ||
+          (e = gemm(L.wk, nullptr, c->pf_x, H, L.attn_norm, L.bk, c->pf_k, KVD, GEMM_STORE)) ||
+          (e = gemm(L.wv, nullptr, c->pf_x, H, L.attn_norm, L.bv, c->pf_v, KVD, GEMM_STORE)) ||
+          (e = launch_rope_kv_rows(c->pf_q, c->pf_k, c->pf_v, c->rope, c->kcache + lo, c->vcache + lo, g.n_heads,
+                                   g.n_kv_heads, g.head_dim, pos0, m, s)) ||
+          (e = launch_attn_rows(c->pf_q, c->kcache + lo, c->vcache + lo, c->pf_att, g.n_heads, g.n_kv_heads,
+                                g.head_dim, pos0, m, scale, s)) ||
+          (e = gemm(L.wo, nullptr, c->pf_att, QD, nullptr, nullptr, c->pf_x, H, GEMM_RESID)) ||
+          (e = launch_row_inv(c->pf_x, m, H, g.rms_eps, c->pf_inv, s)) ||
+          (e = gemm(L.gate, L.up, c->pf_x, H, L.ffn_norm, nullptr, c->pf_act, g.ffn, GEMM_SWIGLU)) ||
+          (e = gemm(L.down, nullptr, c->pf_act, g.ffn, nullptr, nullptr, c->pf_x, H, GEMM_RESID)))
+        return e;
+    }
+  }
+  // last_row_logits (model.rs:594-600) + argmax (generate.rs:69-77)
+  GemvArgs lm{};
+  lm.in = H;
+  lm.x = c->pf_x + (size_t)(m - 1) * H;
+  lm.norm_w = c->out_norm;
+  lm.eps = g.rms_eps;
+  lm.n_seg = 1;
+  lm.seg[0].w = c->lm_head->ptr;
+  lm.seg[0].type = c->lm_head->type;
+  lm.seg[0].rows = (uint32_t)c->lm_head->out;
+  lm.seg[0].row_bytes = (uint32_t)type_row_bytes(c->lm_head->type, c->lm_head->in);
+  lm.seg[0].out = c->logits;
+  lm.best = c->best_part;
+  uint32_t nb = 0;
+  if ((e = launch_gemv(lm, GEMV_ARGMAX, s, &nb))) return e;
+  return launch_prefill_end(c->st, c->best_part, nb, n, s);
+}
+
 extern "C" frn_status frn_prefill(frn_ctx* c, const uint32_t* ids, uint32_t n, uint32_t* next_id) {
   frn_status st;
   if ((st = check_ready(c, n))) return st;
@@ -491,10 +587,15 @@ extern "C" frn_status frn_prefill(frn_ctx* c, const uint32_t* ids, uint32_t n, u
     if (ids[i] >= c->cfg.vocab) return fail(FRN_ETOKEN, "token id %u out of range (vocab %u)", ids[i], c->cfg.vocab);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
   c->last_next = 0xFFFFFFFFu;
-  for (uint32_t i = 0; i < n; ++i) {
-    // per-position token upload: make sure the previous copy has landed
-    if (i) HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-    if ((st = run_step(c, ids[i], i + 1 == n))) return st;
+  if (n == 1 || (c->cfg.flags & FRN_FLAG_STEPWISE_PREFILL)) {  // one decode step per position
+    for (uint32_t i = 0; i < n; ++i) {
+      // per-position token upload: make sure the previous copy has landed
+      if (i) HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+      if ((st = run_step(c, ids[i], i + 1 == n))) return st;
+    }
+  } else {
+    HIP_TRY(prefill_rows(c, ids, n), "prefill");
+    c->len += n;
   }
   return read_next(c, next_id);
 }

@@ -75,4 +75,37 @@ bool attention_supported(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_di
 hipError_t launch_step_end(StepState* st, const uint64_t* best, uint32_t n_best, hipStream_t s);
 hipError_t launch_argmax(const float* x, size_t n, uint64_t* scratch, uint32_t* out, hipStream_t s);
 
+// ---- prefill (prefill.hip) ----------------------------------------------------
+enum GemmMode : int { GEMM_STORE = 0, GEMM_RESID = 1, GEMM_SWIGLU = 2 };
+
+// C[P][N] = A'[P][K] . W[N][K]^T on MFMA; A' = A, or rmsnorm rows of A when
+// inv (per-row factor) and nw (gain) are given.  STORE: out = C (+ bias);
+// RESID: out += C; SWIGLU: out = silu(C(w)) * C(w2).
+struct GemmArgs {
+  const float* a;       // [P][K] f32
+  const float* inv;     // optional [P]
+  const float* nw;      // optional [K]
+  const uint8_t* w;     // [N] rows of row_bytes raw blocks
+  const uint8_t* w2;    // SWIGLU: the up matrix
+  uint32_t type, row_bytes;
+  const float* bias;    // optional [N]
+  float* out;           // [P][ldo]
+  uint32_t ldo, P, N, K;
+};
+hipError_t launch_gemm(const GemmArgs& g, GemmMode mode, hipStream_t s);
+hipError_t launch_embed_rows(const uint8_t* table, uint32_t type, uint32_t hidden, uint32_t row_bytes,
+                             const uint32_t* ids, uint32_t n, float* x, hipStream_t s);
+hipError_t launch_row_inv(const float* x, uint32_t rows, uint32_t cols, float eps, float* inv, hipStream_t s);
+// RoPE of n q rows (in place) and k rows (into the cache) at positions
+// pos0.., v rows into the cache.
+hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const float* rope_cs, float* k_cache,
+                               float* v_cache, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                               uint32_t pos0, uint32_t n, hipStream_t s);
+// Causal attention of n query rows at positions pos0.. over the cache.
+hipError_t launch_attn_rows(const float* q, const float* k_cache, const float* v_cache, float* out, uint32_t n_heads,
+                            uint32_t n_kv_heads, uint32_t head_dim, uint32_t pos0, uint32_t n, float scale,
+                            hipStream_t s);
+// Argmax of the lm_head candidates into next_tok/tok, position += n.
+hipError_t launch_prefill_end(StepState* st, const uint64_t* best, uint32_t n_best, uint32_t n, hipStream_t s);
+
 }  // namespace frn

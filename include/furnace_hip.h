@@ -56,6 +56,9 @@ typedef struct frn_config {
 /* Launch the step's kernels one by one instead of replaying a hipGraph
  * (same kernels; for profilers that do not follow graph launches). */
 #define FRN_FLAG_EAGER 1u
+/* Prefill one decode step per prompt position (the decode kernels) instead
+ * of blocks of rows through the MFMA GEMMs.  For comparisons. */
+#define FRN_FLAG_STEPWISE_PREFILL 2u
 
 typedef struct frn_ctx frn_ctx;
 
@@ -82,7 +85,9 @@ frn_status frn_finalize(frn_ctx* ctx);
 /* Model::forward_cached(&prompt) + Sampler::sample at temperature 0
  * (model.rs:579-592, sampler.rs:91-94, generate.rs:69-77): runs the n ids at
  * positions ctx.len .. ctx.len+n, advances ctx.len by n and writes the
- * argmax of the last position's logits (first maximum on ties). */
+ * argmax of the last position's logits (first maximum on ties).  n >= 2
+ * runs blocks of up to 256 positions through fp32-MFMA GEMMs on the raw
+ * weight blocks (dequantized exactly into LDS tiles). */
 frn_status frn_prefill(frn_ctx* ctx, const uint32_t* ids, uint32_t n, uint32_t* next_id);
 
 /* One decode step: Model::forward_cached(&[id]) + argmax
