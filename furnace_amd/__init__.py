@@ -19,6 +19,7 @@ F32, Q5_0, Q8_0, Q4_K, Q6_K = 0, 6, 8, 12, 14
 BLOCK = {F32: (1, 4), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 
 FLAG_EAGER = 1  # FRN_FLAG_EAGER
+FLAG_STEPWISE_PREFILL = 2  # FRN_FLAG_STEPWISE_PREFILL
 
 MIX_ALL_Q8_0, MIX_Q4_K_M, MIX_ALL_Q4_K, MIX_ALL_Q6_K, MIX_ALL_Q5_0, MIX_ALL_F32 = range(6)
 
@@ -241,7 +242,7 @@ def synth_write(path, seed, threads=0, weight_std=0.02, rope_theta=1e6, rms_eps=
 class Model:
     """A GGUF model loaded onto one GPU: Model::load + KvCache in one context."""
 
-    def __init__(self, path, device=0, max_ctx=4096, eager=False):
+    def __init__(self, path, device=0, max_ctx=4096, eager=False, stepwise_prefill=False):
         lib = load()
         self.gguf = ctypes.c_void_p()
         check(lib.frn_gguf_open(path.encode(), ctypes.byref(self.gguf)))
@@ -250,7 +251,8 @@ class Model:
         check(lib.frn_gguf_config(self.gguf, ctypes.byref(self.cfg), ctypes.byref(ctx_len)))
         self.context_length = ctx_len.value
         self.ctx = ctypes.c_void_p()
-        check(lib.frn_model_load(self.gguf, device, max_ctx, FLAG_EAGER if eager else 0, ctypes.byref(self.ctx)))
+        flags = (FLAG_EAGER if eager else 0) | (FLAG_STEPWISE_PREFILL if stepwise_prefill else 0)
+        check(lib.frn_model_load(self.gguf, device, max_ctx, flags, ctypes.byref(self.ctx)))
         self.cfg.max_ctx = max_ctx
         self.vocab = self.cfg.vocab
 

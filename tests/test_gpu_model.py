@@ -109,3 +109,72 @@ def test_full_model_greedy_ids_and_logits(hip, tmpdir_models, preset, n_prompt):
     assert ids[:N_IDS] == ref_ids[:N_IDS]
     assert np.max(np.abs(got_last - ref_last)) <= LOGIT_TOL
     os.remove(path)
+
+
+def test_7b_greedy_ids_and_logits(hip, tmpdir_models):
+    """Qwen2-7B shape (hidden 3584, FFN 18944, 7 query heads per kv head,
+    untied Q6_K lm_head, Q4_K embedding): a 16-token prompt keeps the
+    oracle's run to seconds; the shapes are the full model's."""
+    path = os.path.join(tmpdir_models, "qwen2-7b-q4_k_m.gguf")
+    print("writing qwen2-7b-q4_k_m", flush=True)
+    fa.synth_write(path, seed=0xF0E1 + 4, threads=min(16, os.cpu_count() or 1), **fa.PRESETS["qwen2-7b-q4_k_m"])
+    prompt = np.random.default_rng(0xF0E1 + 4).integers(0, 151643, 16).astype(np.uint32)
+    orc.set_threads(min(16, os.cpu_count() or 1))
+    print("running 7b prompt 16", flush=True)
+    ids, ref_ids, got_last, ref_last = _greedy_parity(path, prompt, N_IDS + 1, 64)
+    print("gpu ids", ids[:N_IDS], flush=True)
+    print("ref ids", ref_ids[:N_IDS], flush=True)
+    assert ids[:N_IDS] == ref_ids[:N_IDS]
+    assert np.max(np.abs(got_last - ref_last)) <= LOGIT_TOL
+    os.remove(path)
+
+
+def test_long_context_small_model(hip, tmpdir_models):
+    """Past 4096 positions (the long-context workload's length) on a small
+    model, so the oracle's single-threaded attention stays cheap: prefill
+    of 4200 ids in blocks, then decode steps over 66+ attention splits."""
+    cfg = dict(small_models()["tiny-q4_k_m"], n_layers=2, vocab=1000)
+    path = os.path.join(tmpdir_models, "tiny-long.gguf")
+    fa.synth_write(path, seed=31, **cfg)
+    prompt = np.random.default_rng(31).integers(0, cfg["vocab"], 4200).astype(np.uint32)
+    print("long context prompt %d" % prompt.size, flush=True)
+    ref = orc.Model(path)
+    ref.new_cache(4300)
+    ref_logits = ref.forward_cached(prompt)
+    m = fa.Model(path, max_ctx=4300)
+    nxt = m.prefill(prompt)
+    assert np.max(np.abs(m.logits() - ref_logits)) <= LOGIT_TOL
+    tok = orc.argmax(ref_logits)
+    assert nxt == tok
+    for step in range(8):
+        ref_logits = ref.forward_cached([tok])
+        nxt = m.decode(tok)
+        assert np.max(np.abs(m.logits() - ref_logits)) <= LOGIT_TOL, step
+        assert nxt == orc.argmax(ref_logits), step
+        tok = nxt
+    m.close()
+    ref.close()
+
+
+def test_long_context_full_size_paths_agree(hip, tmpdir_models):
+    """The long-context workload's shape (1.5B Q4_K_M, 4096-token prompt) is
+    beyond the oracle's reach in a test, so the two device paths are
+    checked against each other: blocks of rows through the MFMA GEMMs vs
+    one decode step per position, then 16 greedy decode steps from each."""
+    path = os.path.join(tmpdir_models, "qwen2-1.5b-q4_k_m-long.gguf")
+    fa.synth_write(path, seed=0xF0E1 + 3, threads=min(16, os.cpu_count() or 1), **fa.PRESETS["qwen2-1.5b-q4_k_m"])
+    prompt = np.random.default_rng(0xF0E1 + 3).integers(0, 151643, 4096).astype(np.uint32)
+    outs = []
+    for stepwise in (False, True):
+        print("4096-token prefill, stepwise=%s" % stepwise, flush=True)
+        m = fa.Model(path, max_ctx=4096 + 32, stepwise_prefill=stepwise)
+        nxt = m.prefill(prompt)
+        logits = m.logits()
+        ids = [nxt]
+        for _ in range(15):
+            ids.append(m.decode(ids[-1]))
+        m.close()
+        outs.append((logits, ids))
+    assert np.max(np.abs(outs[0][0] - outs[1][0])) <= LOGIT_TOL
+    assert outs[0][1] == outs[1][1]
+    os.remove(path)
