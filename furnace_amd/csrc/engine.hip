@@ -361,7 +361,6 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
     o.st = c->st;
     o.att_ms = attention_splits(g.max_ctx);
     o.att_hd = g.head_dim;
-    o.att_chunk = ATTENTION_CHUNK;
     o.att_part_bytes = (uint32_t)(attention_part_floats(g.n_heads, g.head_dim, g.max_ctx) * 4);
     if (TIMED(CAT_OPROJ, launch_gemv(o, GEMV_RESID_ATT, s))) return e;
     // rmsnorm + gate/up + SwiGLU (model.rs:473-476)

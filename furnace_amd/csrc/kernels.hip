@@ -8,7 +8,10 @@
 namespace frn {
 
 constexpr int ATT_CHUNK = ATTENTION_CHUNK;  // positions per attention block (one wave per softmax row)
-uint32_t attention_splits(uint32_t max_ctx) { return (max_ctx + ATT_CHUNK - 1) / ATT_CHUNK; }
+uint32_t attention_splits(uint32_t max_ctx) {
+  const uint32_t t = (max_ctx + ATT_CHUNK - 1) / ATT_CHUNK;
+  return t < ATTENTION_MAX_SPLITS ? t : ATTENTION_MAX_SPLITS;
+}
 
 // ---- reductions -----------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
@@ -181,14 +184,14 @@ struct XStage {
     const uint32_t h = 8u * u / a.att_hd, d0 = 8u * u % a.att_hd;
     return 4u * ((h * a.att_ms + sp) * (a.att_hd + 2) + d0);
   }
-  __device__ __forceinline__ void load_att(const GemvArgs& a, rsrc_t rp) {
-    ns = a.st->pos / a.att_chunk + 1;
+  __device__ __forceinline__ void load_batch(const GemvArgs& a, rsrc_t rp, uint32_t sp0) {
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
       const uint32_t u = threadIdx.x + 256u * i;
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        const uint32_t o = (u < a.in / 8 && (uint32_t)b < ns) ? part_off(a, u, b) : BUF_INVALID;
+        const uint32_t sp = sp0 + b;
+        const uint32_t o = (u < a.in / 8 && sp < ns) ? part_off(a, u, sp) : BUF_INVALID;
         po[i][b][0] = u4f(bl128(rp, o));
         po[i][b][1] = u4f(bl128(rp, o + 16u));
         const uint2 q = bl64(rp, o == BUF_INVALID ? BUF_INVALID : o - 4u * (8u * u % a.att_hd) + 4u * a.att_hd);
@@ -196,38 +199,52 @@ struct XStage {
       }
     }
   }
+  __device__ __forceinline__ void load_att(const GemvArgs& a, rsrc_t rp) {
+    const uint32_t T = a.st->pos + 1, len = attention_split_len(T);
+    ns = (T + len - 1) / len;
+    load_batch(a, rp, 0);
+  }
   // softmax merge of the splits (model.rs:371-438 evaluated split-wise):
-  // x = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, M = max_s m_s
+  // x = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, M = max_s m_s, one
+  // batch of NB splits at a time (the first batch was loaded up front)
   __device__ __forceinline__ void merge_att(const GemvArgs& a, rsrc_t rp) {
+    float M[NX], L[NX], o[NX][8];
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      const uint32_t u = threadIdx.x + 256u * i;
-      float M = -INFINITY;
+      M[i] = -INFINITY;
+      L[i] = 0.f;
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
-        if ((uint32_t)b < ns) M = fmaxf(M, pm[i][b].x);
-      float L = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < 8; ++k) o[i][k] = 0.f;
+    }
+    for (uint32_t sp0 = 0; sp0 < ns; sp0 += NB) {
+      if (sp0) load_batch(a, rp, sp0);
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const float e = (uint32_t)b < ns ? expf(pm[i][b].x - M) : 0.f;
-        L += e * pm[i][b].y;
-        o[0] += e * po[i][b][0].x; o[1] += e * po[i][b][0].y; o[2] += e * po[i][b][0].z; o[3] += e * po[i][b][0].w;
-        o[4] += e * po[i][b][1].x; o[5] += e * po[i][b][1].y; o[6] += e * po[i][b][1].z; o[7] += e * po[i][b][1].w;
+      for (int i = 0; i < NX; ++i) {
+        float Mb = M[i];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+          if (sp0 + b < ns) Mb = fmaxf(Mb, pm[i][b].x);
+        const float c = expf(M[i] - Mb);  // rescale of the earlier batches (0 when there were none)
+        L[i] *= c;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[i][k] *= c;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const float e = sp0 + b < ns ? expf(pm[i][b].x - Mb) : 0.f;
+          L[i] += e * pm[i][b].y;
+          o[i][0] += e * po[i][b][0].x; o[i][1] += e * po[i][b][0].y;
+          o[i][2] += e * po[i][b][0].z; o[i][3] += e * po[i][b][0].w;
+          o[i][4] += e * po[i][b][1].x; o[i][5] += e * po[i][b][1].y;
+          o[i][6] += e * po[i][b][1].z; o[i][7] += e * po[i][b][1].w;
+        }
+        M[i] = Mb;
       }
-      for (uint32_t sp = NB; sp < ns; ++sp) {  // beyond the first batch: one split at a time
-        const uint32_t off = u < a.in / 8 ? part_off(a, u, sp) : BUF_INVALID;
-        const float4 p0 = u4f(bl128(rp, off)), p1 = u4f(bl128(rp, off + 16u));
-        const uint2 q = bl64(rp, off == BUF_INVALID ? BUF_INVALID : off - 4u * (8u * u % a.att_hd) + 4u * a.att_hd);
-        const float m = __uint_as_float(q.x), l = __uint_as_float(q.y);
-        const float Mn = fmaxf(M, m), c = expf(M - Mn), e = expf(m - Mn);
-        M = Mn;
-        L = L * c + e * l;
-        o[0] = o[0] * c + e * p0.x; o[1] = o[1] * c + e * p0.y; o[2] = o[2] * c + e * p0.z; o[3] = o[3] * c + e * p0.w;
-        o[4] = o[4] * c + e * p1.x; o[5] = o[5] * c + e * p1.y; o[6] = o[6] * c + e * p1.z; o[7] = o[7] * c + e * p1.w;
-      }
-      const float il = L > 0.f ? 1.0f / L : 0.f;
-      x[i][0] = make_float4(o[0] * il, o[1] * il, o[2] * il, o[3] * il);
-      x[i][1] = make_float4(o[4] * il, o[5] * il, o[6] * il, o[7] * il);
+    }
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const float il = L[i] > 0.f ? 1.0f / L[i] : 0.f;
+      x[i][0] = make_float4(o[i][0] * il, o[i][1] * il, o[i][2] * il, o[i][3] * il);
+      x[i][1] = make_float4(o[i][4] * il, o[i][5] * il, o[i][6] * il, o[i][7] * il);
     }
   }
   __device__ __forceinline__ void load(rsrc_t rx, rsrc_t rn) {
@@ -731,15 +748,17 @@ hipError_t launch_embed(const uint8_t* table, uint32_t type, uint32_t hidden, ui
 }
 
 // ---- decode attention (model.rs:193-217, 346-356, 371-438) ---------------------
-// One launch per layer.  Block (kv head g, split s) covers positions
-// [64 s, 64 s + 64) for the GQ query heads sharing g:
+// One launch per layer.  Block (kv head g, split s) covers the split's
+// positions (attention_split_len(pos + 1) of them, in sub-tiles of 64) for
+// the GQ query heads sharing g:
 //  - rotates those query heads and head g's new key at the step position
 //    (rope_cs holds cos[hd/2] | sin[hd/2] per position, computed on the host
 //    with the CPU path's powf/sinf/cosf; the rotation is evaluated without
 //    FMA contraction, so q/k match the CPU bit for bit given equal inputs);
 //  - the block holding the step position appends head g's k/v to the cache;
-//  - scores, chunk softmax and P.V from K rows in registers and V rows in
-//    LDS; every global load of the block is issued before any is used;
+//  - per sub-tile: scores from K rows in registers, softmax with the
+//    running max and sum of the split, P.V from V rows in LDS; the next
+//    sub-tile's rows are loaded while this one's softmax and P.V run;
 //  - writes its partial (o = sum_t e^(s_t - m) v_t, m, l = sum_t e^(s_t - m))
 //    per query head to `part`; the o-proj GEMV (GEMV_RESID_ATT) merges the
 //    splits while it stages its input, so no block waits on another here.
@@ -755,22 +774,28 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
   __shared__ float kcur[HD], vcur[HD];
   __shared__ __align__(16) float vs[C * HD];
   __shared__ __align__(16) float ps[GQ * C];
-  __shared__ float ml[GQ * 2];
+  __shared__ float mrun[GQ], lrun[GQ], rescale[GQ];
   __shared__ float osum[PARTS * GQ * HD];
-  const uint32_t pos = st->pos, T = pos + 1, g = blockIdx.x, split = blockIdx.y, t0 = split * C;
+  const uint32_t pos = st->pos, T = pos + 1, g = blockIdx.x, split = blockIdx.y;
+  const uint32_t len = attention_split_len(T), t0 = split * len;
   if (t0 >= T) return;
-  const uint32_t n = min((uint32_t)C, T - t0), ns = (T + C - 1) / C;
+  const uint32_t ns = (T + len - 1) / len, tend = min(t0 + len, T), nsub = (tend - t0 + C - 1) / C;
   const size_t kvd = (size_t)nkv * HD;
   const int p = threadIdx.x / TPP, sub = threadIdx.x % TPP;
-  const uint32_t tp = t0 + p;
-  const bool valid = (uint32_t)p < n, cur = valid && tp == pos;
-  // cached rows (positions < pos); the step's own row comes from kcur/vcur
-  const size_t off = (size_t)((valid && !cur) ? tp : 0) * kvd + (size_t)g * HD + sub * DPT;
+  // cached rows (positions < pos) of sub-tile k; the step's own row comes
+  // from kcur/vcur, rows past the split are not used
+  auto row_off = [&](uint32_t k) -> size_t {
+    const uint32_t tp = t0 + k * C + p;
+    return (size_t)((tp < tend && tp != pos) ? tp : 0) * kvd + (size_t)g * HD + sub * DPT;
+  };
   float4 kr[DPT / 4], vr[DPT / 4];
+  {
+    const size_t off = row_off(0);
 #pragma unroll
-  for (int i = 0; i < DPT / 4; ++i) {
-    kr[i] = ((const float4*)(kc + off))[i];
-    vr[i] = ((const float4*)(vc + off))[i];
+    for (int i = 0; i < DPT / 4; ++i) {
+      kr[i] = ((const float4*)(kc + off))[i];
+      vr[i] = ((const float4*)(vc + off))[i];
+    }
   }
   // rotation inputs: pair i < GQ*HALF of the query heads, then HALF of the key
   const float* cr = cs + (size_t)pos * HD;
@@ -800,64 +825,81 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     }
   }
   if (threadIdx.x < HD) vcur[threadIdx.x] = vnew;
+  if (threadIdx.x < GQ) {
+    mrun[threadIdx.x] = -INFINITY;
+    lrun[threadIdx.x] = 0.f;
+  }
   __syncthreads();
   if (split == ns - 1)  // KvCache::append of head g at pos
     for (int d = threadIdx.x; d < HD; d += 256) {
       kc[(size_t)pos * kvd + (size_t)g * HD + d] = kcur[d];
       vc[(size_t)pos * kvd + (size_t)g * HD + d] = vcur[d];
     }
-  if (cur) {
+  const int d = threadIdx.x % HD, prt = threadIdx.x / HD, wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float acc[GQ];
 #pragma unroll
-    for (int i = 0; i < DPT / 4; ++i) {
-      kr[i] = ((const float4*)(kcur + sub * DPT))[i];
-      vr[i] = ((const float4*)(vcur + sub * DPT))[i];
-    }
-  }
+  for (int h = 0; h < GQ; ++h) acc[h] = 0.f;
+  for (uint32_t k = 0; k < nsub; ++k) {
+    const uint32_t tp = t0 + k * C + p;
+    const bool valid = tp < tend, cur = valid && tp == pos;
+    if (cur) {
 #pragma unroll
-  for (int i = 0; i < DPT / 4; ++i)
-    ((float4*)(vs + p * HD + sub * DPT))[i] = valid ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-  {  // scores of position p for all GQ heads at once (independent accumulators)
-    float sc[GQ];
-#pragma unroll
-    for (int h = 0; h < GQ; ++h) sc[h] = 0.f;
-#pragma unroll
-    for (int i = 0; i < DPT / 4; ++i) {
-      const float4 a = kr[i];
-#pragma unroll
-      for (int h = 0; h < GQ; ++h) {
-        const float4 b = ((const float4*)(qs + h * HD + sub * DPT))[i];
-        sc[h] += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+      for (int i = 0; i < DPT / 4; ++i) {
+        kr[i] = ((const float4*)(kcur + sub * DPT))[i];
+        vr[i] = ((const float4*)(vcur + sub * DPT))[i];
       }
     }
 #pragma unroll
-    for (int o = TPP / 2; o > 0; o >>= 1)
+    for (int i = 0; i < DPT / 4; ++i)
+      ((float4*)(vs + p * HD + sub * DPT))[i] = valid ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    {  // scores of position tp for all GQ heads at once (independent accumulators)
+      float sc[GQ];
 #pragma unroll
-      for (int h = 0; h < GQ; ++h) sc[h] += __shfl_xor(sc[h], o, TPP);
-    if (sub == 0)
+      for (int h = 0; h < GQ; ++h) sc[h] = 0.f;
 #pragma unroll
-      for (int h = 0; h < GQ; ++h) ps[h * C + p] = valid ? sc[h] * scale : -INFINITY;  // model.rs:397
-  }
-  __syncthreads();
-  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  for (int h = wv; h < GQ; h += 4) {  // C == 64: one wave per softmax row
-    float v = ps[h * C + lane];
-    float m = wave_max(v);
-    float e = expf(v - m);
-    ps[h * C + lane] = e;
-    float l = wave_sum(e);
-    if (lane == 0) {
-      ml[2 * h] = m;
-      ml[2 * h + 1] = l;
+      for (int i = 0; i < DPT / 4; ++i) {
+        const float4 a = kr[i];
+#pragma unroll
+        for (int h = 0; h < GQ; ++h) {
+          const float4 b = ((const float4*)(qs + h * HD + sub * DPT))[i];
+          sc[h] += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+        }
+      }
+#pragma unroll
+      for (int o = TPP / 2; o > 0; o >>= 1)
+#pragma unroll
+        for (int h = 0; h < GQ; ++h) sc[h] += __shfl_xor(sc[h], o, TPP);
+      if (sub == 0)
+#pragma unroll
+        for (int h = 0; h < GQ; ++h) ps[h * C + p] = valid ? sc[h] * scale : -INFINITY;  // model.rs:397
     }
-  }
-  __syncthreads();
-  // P.V: thread (d, prt) sums positions [NP prt, NP prt + NP) for all GQ
-  // heads; masked positions have p = 0 and zero V rows
-  const int d = threadIdx.x % HD, prt = threadIdx.x / HD;
-  {
-    float acc[GQ];
+    if (k + 1 < nsub) {  // the next sub-tile's rows, in flight during this one's softmax and P.V
+      const size_t off = row_off(k + 1);
 #pragma unroll
-    for (int h = 0; h < GQ; ++h) acc[h] = 0.f;
+      for (int i = 0; i < DPT / 4; ++i) {
+        kr[i] = ((const float4*)(kc + off))[i];
+        vr[i] = ((const float4*)(vc + off))[i];
+      }
+    }
+    __syncthreads();
+    for (int h = wv; h < GQ; h += 4) {  // C == 64: one wave per softmax row, running max and sum
+      const float v = ps[h * C + lane];
+      const float m = fmaxf(wave_max(v), mrun[h]);
+      const float e = expf(v - m);
+      ps[h * C + lane] = e;
+      const float l = wave_sum(e);
+      if (lane == 0) {
+        const float c = expf(mrun[h] - m);
+        rescale[h] = c;
+        lrun[h] = lrun[h] * c + l;
+        mrun[h] = m;
+      }
+    }
+    __syncthreads();
+    // P.V: thread (d, prt) sums positions [NP prt, NP prt + NP) of the
+    // sub-tile for all GQ heads; masked positions have p = 0, zero V rows
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) acc[h] *= rescale[h];
 #pragma unroll
     for (int j = 0; j < NP; j += 4) {
       const int t = prt * NP + j;
@@ -868,9 +910,10 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
         acc[h] += pp.x * v0 + pp.y * v1 + pp.z * v2 + pp.w * v3;
       }
     }
-#pragma unroll
-    for (int h = 0; h < GQ; ++h) osum[(prt * GQ + h) * HD + d] = acc[h];
+    __syncthreads();  // vs and ps are rewritten by the next sub-tile
   }
+#pragma unroll
+  for (int h = 0; h < GQ; ++h) osum[(prt * GQ + h) * HD + d] = acc[h];
   __syncthreads();
   for (int i = threadIdx.x; i < GQ * HD; i += 256) {
     int h = i / HD, dd = i % HD;
@@ -880,8 +923,8 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     float* dst = part + ((size_t)(g * GQ + h) * max_splits + split) * (HD + 2);
     dst[dd] = o;
     if (dd == 0) {
-      dst[HD] = ml[2 * h];
-      dst[HD + 1] = ml[2 * h + 1];
+      dst[HD] = mrun[h];
+      dst[HD + 1] = lrun[h];
     }
   }
 }

@@ -41,10 +41,11 @@ struct GemvArgs {
   float eps;
   uint64_t* best;       // ARGMAX: one packed (logit, ~row) candidate per block
   // RESID_ATT: partials [n_heads][att_ms][att_hd + 2] = (o[att_hd], m, l) of
-  // splits of att_chunk positions; the number of splits follows st->pos
+  // the step's splits (attention_split_len positions each; st->pos + 1
+  // positions in all)
   const float* att_part;
   const StepState* st;
-  uint32_t att_ms, att_hd, att_chunk, att_part_bytes;
+  uint32_t att_ms, att_hd, att_part_bytes;
 };
 
 hipError_t launch_dequant(uint32_t type, const uint8_t* raw, size_t n_elems, float* out, hipStream_t s);
@@ -65,8 +66,16 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, cons
                             float* v_cache, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                             uint32_t max_ctx, float scale, float* part, const StepState* st, hipStream_t s);
 size_t attention_part_floats(uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx);
-uint32_t attention_splits(uint32_t max_ctx);  // att_ms
-constexpr uint32_t ATTENTION_CHUNK = 64;      // att_chunk
+uint32_t attention_splits(uint32_t max_ctx);  // att_ms: the most splits a step can have
+constexpr uint32_t ATTENTION_CHUNK = 64;      // positions per attention sub-tile
+constexpr uint32_t ATTENTION_MAX_SPLITS = 16;
+// Positions per split for a step over T positions: whole 64-position
+// sub-tiles, as few as keep the step at <= 16 splits (the merge of the
+// splits then stays one or two batches of loads).
+__host__ __device__ inline uint32_t attention_split_len(uint32_t T) {
+  const uint32_t tiles = (T + ATTENTION_CHUNK - 1) / ATTENTION_CHUNK;
+  return ATTENTION_CHUNK * ((tiles + ATTENTION_MAX_SPLITS - 1) / ATTENTION_MAX_SPLITS);
+}
 // Shapes the attention kernel handles: head_dim 64 or 128, at most 8 query
 // heads per kv head.
 bool attention_supported(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
