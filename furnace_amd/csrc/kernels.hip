@@ -199,10 +199,14 @@ struct XStage {
       }
     }
   }
+  // the first batch is loaded before the step position is known (splits
+  // past the step's count are loaded and then ignored), so its loads
+  // overlap the read of st->pos
   __device__ __forceinline__ void load_att(const GemvArgs& a, rsrc_t rp) {
+    ns = NB;
+    load_batch(a, rp, 0);
     const uint32_t T = a.st->pos + 1, len = attention_split_len(T);
     ns = (T + len - 1) / len;
-    load_batch(a, rp, 0);
   }
   // softmax merge of the splits (model.rs:371-438 evaluated split-wise):
   // x = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, M = max_s m_s, one
@@ -230,7 +234,10 @@ struct XStage {
         for (int k = 0; k < 8; ++k) o[i][k] *= c;
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-          const float e = sp0 + b < ns ? expf(pm[i][b].x - Mb) : 0.f;
+          // splits past the step's count were loaded before the count was
+          // known and may hold anything (even NaN): select, do not scale
+          if (sp0 + b >= ns) continue;
+          const float e = expf(pm[i][b].x - Mb);
           L[i] += e * pm[i][b].y;
           o[i][0] += e * po[i][b][0].x; o[i][1] += e * po[i][b][0].y;
           o[i][2] += e * po[i][b][0].z; o[i][3] += e * po[i][b][0].w;
@@ -363,7 +370,7 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
 // row loads items (s * BI + j) * LPR + gl, j < BI.  The steps of all the
 // wave's units form one flat pipeline: the loads of step f + 1 are issued
 // before step f is computed, and the first step's before the staging.
-template <uint32_t T, int LPR, int MODE, int NX, bool NORM>
+template <uint32_t T, int LPR, int MODE, int NX, bool NORM, bool ONE>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, uint32_t blk, uint32_t nblk,
                                           float* xf, uint8_t* pl, float* red4, uint64_t* best_s) {
   using F = Fmt<T>;
@@ -486,6 +493,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
       u += stride;
     }
   };
+  // depth 2: step f + 1's loads in flight while step f is computed (ra
+  // holds step 0 on entry)
   auto run = [&](auto&& xget) {
     for (uint32_t f = 0; f < n_steps; f += 2) {
       issue(iu, is, rb, eb);  // past the wave's last step: rows past the end, loads of zeros
@@ -499,12 +508,16 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
       next(cu, cs);
     }
   };
+  // ONE (one step per unit, S == 1, chosen by the host): the activation
+  // chunks go to registers when the format allows.  (A third buffer in
+  // flight for the multi-step launches measured slower: more registers,
+  // and their steps are not bound by memory latency.)
   issue(iu, is, ra, ea);
   next(iu, is);
   __builtin_amdgcn_sched_barrier(0);
   if (ATT) xs.merge_att(a, rp);
   xs.finish(a.in, a.norm_w != nullptr, a.eps, xf, pl, red4);
-  if (PRELOAD && S == 1) {
+  if constexpr (ONE && PRELOAD) {
     // one step per unit: the lane reads the same items of every row it
     // visits, so their staged chunks are read from LDS once, into registers
     XT xr[BI][NCX];
@@ -540,7 +553,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
 // NX: 8-value groups of x per thread (in <= 2048 * NX); NORM: rmsnorm
 // support (only the small-in kernels, where the norms occur).  MODE
 // GEMV_RESID_ATT stages x from the attention partials (in <= 4096).
-template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX>
+template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX, bool ONE>
 __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
   constexpr bool NORM = NX <= 2;
   extern __shared__ float4 smem4[];
@@ -555,9 +568,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
   const uint32_t blk = blockIdx.x - sg.block0;
   const uint32_t nblk = (si + 1 < a.n_seg ? a.seg[si + 1].block0 : gridDim.x) - sg.block0;
   if (T0 == T1 || sg.type == T0)
-    gemv_body<T0, LPR, MODE, NX, NORM>(a, sg, blk, nblk, xf, pl, red4, best_s);
+    gemv_body<T0, LPR, MODE, NX, NORM, ONE>(a, sg, blk, nblk, xf, pl, red4, best_s);
   else
-    gemv_body<T1, LPR, MODE, NX, NORM>(a, sg, blk, nblk, xf, pl, red4, best_s);
+    gemv_body<T1, LPR, MODE, NX, NORM, ONE>(a, sg, blk, nblk, xf, pl, red4, best_s);
 }
 
 // LDS of a launch: x as f32, then the int8 form's 4 planes of `in` bytes
@@ -565,13 +578,13 @@ __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
 size_t gemv_lds_bytes(uint32_t in, bool) { return (size_t)in * (in <= 4096 ? 8 : 4) + in / 4; }
 
 
-// Lanes per row: the choice in {16, 32, 64} that keeps the most lanes busy
+// Lanes per row: the choice in {16, 64} that keeps the most lanes busy
 // on real items, counting at most the 2048 waves that are resident at once
 // (ties: fewer lanes, so fewer blocks stage x).
 static int lanes_per_row(uint32_t total_rows, uint32_t type, int mode, int n_items) {
   int best_l = 16;
   double best_score = -1.0;
-  for (int l = 16; l <= 64; l *= 2) {
+  for (int l = 16; l <= 64; l *= 4) {
     double waves = (double)total_rows * l / 64.0;
     if (waves > 2048.0) waves = 2048.0;
     int slots = l * gemv_bi(type, mode);
@@ -620,12 +633,13 @@ uint32_t gemv_blocks(uint32_t type, uint32_t rows, uint32_t in) {
   return want < cap ? want : cap;
 }
 
-template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX>
+template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX, bool ONE>
 static hipError_t go(GemvArgs a, hipStream_t s, uint32_t* nblocks) {
   uint32_t total = plan_blocks(a, 64 / LPR);
   if (nblocks) *nblocks = total;
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL((k_gemv<T0, T1, LPR, MODE, NX>), dim3(total), dim3(256), gemv_lds_bytes(a.in, false), s, a);
+  hipLaunchKernelGGL((k_gemv<T0, T1, LPR, MODE, NX, ONE>), dim3(total), dim3(256), gemv_lds_bytes(a.in, false), s,
+                     a);
   return hipGetLastError();
 }
 
@@ -633,10 +647,12 @@ static hipError_t go(GemvArgs a, hipStream_t s, uint32_t* nblocks) {
 // rmsnorm and only for STORE/RESID, in <= 20480 (the FFN down projection).
 template <uint32_t T0, uint32_t T1, int MODE, int LPR>
 static hipError_t pick_nx(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
-  if (a.in <= 2048) return go<T0, T1, LPR, MODE, 1>(a, s, nb);
-  if (a.in <= 4096) return go<T0, T1, LPR, MODE, 2>(a, s, nb);
+  const int n_items = items_per_row(T0, a.in, ((a.in / 32) % 2) == 0);
+  const bool one = n_items <= LPR * gemv_bi(T0, MODE);  // one step per unit
+  if (a.in <= 2048) return one ? go<T0, T1, LPR, MODE, 1, true>(a, s, nb) : go<T0, T1, LPR, MODE, 1, false>(a, s, nb);
+  if (a.in <= 4096) return one ? go<T0, T1, LPR, MODE, 2, true>(a, s, nb) : go<T0, T1, LPR, MODE, 2, false>(a, s, nb);
   if constexpr (MODE == GEMV_STORE || MODE == GEMV_RESID)
-    if (a.norm_w == nullptr && a.in <= 20480) return go<T0, T1, LPR, MODE, 10>(a, s, nb);
+    if (a.norm_w == nullptr && a.in <= 20480) return go<T0, T1, LPR, MODE, 10, false>(a, s, nb);
   return hipErrorInvalidValue;
 }
 
@@ -646,7 +662,6 @@ static hipError_t pick_lpr(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
   for (int i = 0; i < a.n_seg; ++i) rows += a.seg[i].rows;
   int lpr = lanes_per_row(rows, a.seg[0].type, MODE, items_per_row(a.seg[0].type, a.in, ((a.in / 32) % 2) == 0));
   if (lpr == 16) return pick_nx<T0, T1, MODE, 16>(a, s, nb);
-  if (lpr == 32) return pick_nx<T0, T1, MODE, 32>(a, s, nb);
   return pick_nx<T0, T1, MODE, 64>(a, s, nb);
 }
 
@@ -709,14 +724,14 @@ template <uint32_t T0, uint32_t T1, int LPR>
 static hipError_t prep_one(int bytes) {
   hipError_t e;
   const auto attr = hipFuncAttributeMaxDynamicSharedMemorySize;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 10>, attr, bytes))) return e;
-  return hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 10>, attr, bytes);
+  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 10, false>, attr, bytes))) return e;
+  return hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 10, false>, attr, bytes);
 }
 
 template <uint32_t T0, uint32_t T1>
 static hipError_t prep_types(int bytes) {
   hipError_t e;
-  if ((e = prep_one<T0, T1, 16>(bytes)) || (e = prep_one<T0, T1, 32>(bytes))) return e;
+  if ((e = prep_one<T0, T1, 16>(bytes))) return e;
   return prep_one<T0, T1, 64>(bytes);
 }
 
@@ -766,7 +781,7 @@ template <int HD, int GQ>
 __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, const float* __restrict__ kn,
                                                    const float* __restrict__ vn, const float* __restrict__ cs,
                                                    float* __restrict__ kc, float* __restrict__ vc, uint32_t nh,
-                                                   uint32_t nkv, uint32_t max_splits, float scale,
+                                                   uint32_t nkv, uint32_t max_splits, uint32_t max_ctx, float scale,
                                                    float* __restrict__ part, const StepState* st) {
   constexpr int C = ATT_CHUNK, TPP = 256 / C, DPT = HD / TPP, PARTS = 256 / HD, HALF = HD / 2, NP = C / PARTS;
   constexpr int RR = (GQ * HALF + HALF + 255) / 256;  // rotation rounds per thread
@@ -776,21 +791,17 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
   __shared__ __align__(16) float ps[GQ * C];
   __shared__ float mrun[GQ], lrun[GQ], rescale[GQ];
   __shared__ float osum[PARTS * GQ * HD];
-  const uint32_t pos = st->pos, T = pos + 1, g = blockIdx.x, split = blockIdx.y;
-  const uint32_t len = attention_split_len(T), t0 = split * len;
-  if (t0 >= T) return;
-  const uint32_t ns = (T + len - 1) / len, tend = min(t0 + len, T), nsub = (tend - t0 + C - 1) / C;
+  const uint32_t g = blockIdx.x, split = blockIdx.y;
   const size_t kvd = (size_t)nkv * HD;
   const int p = threadIdx.x / TPP, sub = threadIdx.x % TPP;
-  // cached rows (positions < pos) of sub-tile k; the step's own row comes
-  // from kcur/vcur, rows past the split are not used
-  auto row_off = [&](uint32_t k) -> size_t {
-    const uint32_t tp = t0 + k * C + p;
-    return (size_t)((tp < tend && tp != pos) ? tp : 0) * kvd + (size_t)g * HD + sub * DPT;
-  };
+  // Loads that do not depend on the step position go first, so they overlap
+  // the read of st->pos: the first sub-tile's K/V rows as if the split
+  // were 64 positions (it is, up to 1024 positions; rows at or past the
+  // position are masked or replaced below), and the rotation's q/k inputs.
   float4 kr[DPT / 4], vr[DPT / 4];
   {
-    const size_t off = row_off(0);
+    const uint32_t tp = split * C + p;
+    const size_t off = (size_t)(tp < max_ctx ? tp : 0) * kvd + (size_t)g * HD + sub * DPT;
 #pragma unroll
     for (int i = 0; i < DPT / 4; ++i) {
       kr[i] = ((const float4*)(kc + off))[i];
@@ -798,7 +809,6 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     }
   }
   // rotation inputs: pair i < GQ*HALF of the query heads, then HALF of the key
-  const float* cr = cs + (size_t)pos * HD;
   float ra[RR], rb[RR], rc[RR], rs[RR];
 #pragma unroll
   for (int r = 0; r < RR; ++r) {
@@ -808,10 +818,35 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     const float* src = h < GQ ? q + (size_t)(g * GQ + h) * HD : kn + (size_t)g * HD;
     ra[r] = src[j];
     rb[r] = src[j + HALF];
+  }
+  const float vnew = vn[(size_t)g * HD + (threadIdx.x % HD)];
+  const uint32_t pos = st->pos, T = pos + 1;
+  const uint32_t len = attention_split_len(T), t0 = split * len;
+  if (t0 >= T) return;
+  const uint32_t ns = (T + len - 1) / len, tend = min(t0 + len, T), nsub = (tend - t0 + C - 1) / C;
+  // cached rows (positions < pos) of sub-tile k; the step's own row comes
+  // from kcur/vcur, rows past the split are not used
+  auto row_off = [&](uint32_t k) -> size_t {
+    const uint32_t tp = t0 + k * C + p;
+    return (size_t)((tp < tend && tp != pos) ? tp : 0) * kvd + (size_t)g * HD + sub * DPT;
+  };
+  if (len != C) {  // longer splits: the first sub-tile starts elsewhere
+    const size_t off = row_off(0);
+#pragma unroll
+    for (int i = 0; i < DPT / 4; ++i) {
+      kr[i] = ((const float4*)(kc + off))[i];
+      vr[i] = ((const float4*)(vc + off))[i];
+    }
+  }
+  const float* cr = cs + (size_t)pos * HD;
+#pragma unroll
+  for (int r = 0; r < RR; ++r) {
+    int i = threadIdx.x + 256 * r;
+    if (i >= GQ * HALF + HALF) i = 0;
+    const int j = i % HALF;
     rc[r] = cr[j];
     rs[r] = cr[HALF + j];
   }
-  const float vnew = vn[(size_t)g * HD + (threadIdx.x % HD)];
 #pragma unroll
   for (int r = 0; r < RR; ++r) {
     const int i = threadIdx.x + 256 * r;
@@ -935,18 +970,19 @@ size_t attention_part_floats(uint32_t nh, uint32_t hd, uint32_t max_ctx) {
 
 template <int HD, int GQ>
 static void att_go(dim3 grid, hipStream_t s, const float* q, const float* k, const float* v, const float* cs,
-                   float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms, float scale, float* part,
-                   const StepState* st) {
-  hipLaunchKernelGGL((k_attention<HD, GQ>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, scale, part, st);
+                   float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms, uint32_t max_ctx, float scale,
+                   float* part, const StepState* st) {
+  hipLaunchKernelGGL((k_attention<HD, GQ>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale,
+                     part, st);
 }
 
 template <int HD>
 static hipError_t att_gq(uint32_t gq, dim3 grid, hipStream_t s, const float* q, const float* k, const float* v,
-                         const float* cs, float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms, float scale,
-                         float* part, const StepState* st) {
+                         const float* cs, float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms,
+                         uint32_t max_ctx, float scale, float* part, const StepState* st) {
   switch (gq) {
 #define FRN_ATT_GQ(n) \
-  case n: att_go<HD, n>(grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, scale, part, st); break;
+  case n: att_go<HD, n>(grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st); break;
     FRN_ATT_GQ(1) FRN_ATT_GQ(2) FRN_ATT_GQ(3) FRN_ATT_GQ(4) FRN_ATT_GQ(5) FRN_ATT_GQ(6) FRN_ATT_GQ(7) FRN_ATT_GQ(8)
 #undef FRN_ATT_GQ
     default: return hipErrorInvalidValue;
@@ -965,8 +1001,8 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, cons
   if (!attention_supported(nh, nkv, hd)) return hipErrorInvalidValue;
   uint32_t ms = attention_splits(max_ctx), gq = nh / nkv;
   dim3 grid(nkv, ms);
-  if (hd == 128) return att_gq<128>(gq, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, scale, part, st);
-  return att_gq<64>(gq, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, scale, part, st);
+  if (hd == 128) return att_gq<128>(gq, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st);
+  return att_gq<64>(gq, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st);
 }
 
 // ---- step bookkeeping and argmax (generate.rs:69-77) ------------------------
