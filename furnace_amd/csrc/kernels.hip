@@ -785,8 +785,15 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
                                                    float* __restrict__ part, const StepState* st) {
   constexpr int C = ATT_CHUNK, TPP = 256 / C, DPT = HD / TPP, PARTS = 256 / HD, HALF = HD / 2, NP = C / PARTS;
   constexpr int RR = (GQ * HALF + HALF + 255) / 256;  // rotation rounds per thread
+  // global loads: thread t moves float4 column lc of rows lr + RPI*i, so a
+  // wave reads whole rows (contiguous 512 B for hd 128) per instruction
+  constexpr int NC4 = HD / 4, RPI = 256 / NC4, LD = C / RPI;
+  // K rows in LDS are padded to a stride of 64 mod 256 bytes: the score
+  // reads (4 lanes per row, interleaved float4 columns) hit distinct banks
+  constexpr int KLD = HD + 16;
   __shared__ __align__(16) float qs[GQ * HD];
-  __shared__ float kcur[HD], vcur[HD];
+  __shared__ __align__(16) float kcur[HD], vcur[HD];
+  __shared__ __align__(16) float ks[C * KLD];
   __shared__ __align__(16) float vs[C * HD];
   __shared__ __align__(16) float ps[GQ * C];
   __shared__ float mrun[GQ], lrun[GQ], rescale[GQ];
@@ -794,19 +801,18 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
   const uint32_t g = blockIdx.x, split = blockIdx.y;
   const size_t kvd = (size_t)nkv * HD;
   const int p = threadIdx.x / TPP, sub = threadIdx.x % TPP;
+  const int lc = threadIdx.x % NC4, lr = threadIdx.x / NC4;
   // Loads that do not depend on the step position go first, so they overlap
   // the read of st->pos: the first sub-tile's K/V rows as if the split
   // were 64 positions (it is, up to 1024 positions; rows at or past the
   // position are masked or replaced below), and the rotation's q/k inputs.
-  float4 kr[DPT / 4], vr[DPT / 4];
-  {
-    const uint32_t tp = split * C + p;
-    const size_t off = (size_t)(tp < max_ctx ? tp : 0) * kvd + (size_t)g * HD + sub * DPT;
+  float4 kr[LD], vr[LD];
 #pragma unroll
-    for (int i = 0; i < DPT / 4; ++i) {
-      kr[i] = ((const float4*)(kc + off))[i];
-      vr[i] = ((const float4*)(vc + off))[i];
-    }
+  for (int i = 0; i < LD; ++i) {
+    const uint32_t tp = split * C + lr + RPI * i;
+    const size_t off = (size_t)(tp < max_ctx ? tp : 0) * kvd + (size_t)g * HD + 4 * lc;
+    kr[i] = *(const float4*)(kc + off);
+    vr[i] = *(const float4*)(vc + off);
   }
   // rotation inputs: pair i < GQ*HALF of the query heads, then HALF of the key
   float ra[RR], rb[RR], rc[RR], rs[RR];
@@ -824,20 +830,18 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
   const uint32_t len = attention_split_len(T), t0 = split * len;
   if (t0 >= T) return;
   const uint32_t ns = (T + len - 1) / len, tend = min(t0 + len, T), nsub = (tend - t0 + C - 1) / C;
-  // cached rows (positions < pos) of sub-tile k; the step's own row comes
-  // from kcur/vcur, rows past the split are not used
-  auto row_off = [&](uint32_t k) -> size_t {
-    const uint32_t tp = t0 + k * C + p;
-    return (size_t)((tp < tend && tp != pos) ? tp : 0) * kvd + (size_t)g * HD + sub * DPT;
-  };
-  if (len != C) {  // longer splits: the first sub-tile starts elsewhere
-    const size_t off = row_off(0);
+  // rows of sub-tile k this thread loads: cached positions < pos only; the
+  // step's own row comes from kcur/vcur, rows past the split are not used
+  auto load_tile = [&](uint32_t k) {
 #pragma unroll
-    for (int i = 0; i < DPT / 4; ++i) {
-      kr[i] = ((const float4*)(kc + off))[i];
-      vr[i] = ((const float4*)(vc + off))[i];
+    for (int i = 0; i < LD; ++i) {
+      const uint32_t tp = t0 + k * C + lr + RPI * i;
+      const size_t off = (size_t)((tp < tend && tp != pos) ? tp : 0) * kvd + (size_t)g * HD + 4 * lc;
+      kr[i] = *(const float4*)(kc + off);
+      vr[i] = *(const float4*)(vc + off);
     }
-  }
+  };
+  if (len != C) load_tile(0);  // longer splits: the first sub-tile starts elsewhere
   const float* cr = cs + (size_t)pos * HD;
 #pragma unroll
   for (int r = 0; r < RR; ++r) {
@@ -875,28 +879,32 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
 #pragma unroll
   for (int h = 0; h < GQ; ++h) acc[h] = 0.f;
   for (uint32_t k = 0; k < nsub; ++k) {
-    const uint32_t tp = t0 + k * C + p;
-    const bool valid = tp < tend, cur = valid && tp == pos;
-    if (cur) {
+    // the sub-tile's rows to LDS (the step's own row from kcur/vcur, V rows
+    // past the split as zeros), then the next sub-tile's loads go out
 #pragma unroll
-      for (int i = 0; i < DPT / 4; ++i) {
-        kr[i] = ((const float4*)(kcur + sub * DPT))[i];
-        vr[i] = ((const float4*)(vcur + sub * DPT))[i];
-      }
+    for (int i = 0; i < LD; ++i) {
+      const int row = lr + RPI * i;
+      const uint32_t tp = t0 + k * C + row;
+      const bool valid = tp < tend, cur = valid && tp == pos;
+      const float4 kv = cur ? ((const float4*)kcur)[lc] : kr[i];
+      const float4 vv = cur ? ((const float4*)vcur)[lc] : valid ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      *(float4*)(ks + row * KLD + 4 * lc) = kv;
+      *(float4*)(vs + row * HD + 4 * lc) = vv;
     }
-#pragma unroll
-    for (int i = 0; i < DPT / 4; ++i)
-      ((float4*)(vs + p * HD + sub * DPT))[i] = valid ? vr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    {  // scores of position tp for all GQ heads at once (independent accumulators)
+    if (k + 1 < nsub) load_tile(k + 1);  // in flight during this sub-tile's scores, softmax and P.V
+    __syncthreads();
+    {  // scores of position t0 + kC + p for all GQ heads at once (independent accumulators)
+      const bool valid = t0 + k * C + p < tend;
       float sc[GQ];
 #pragma unroll
       for (int h = 0; h < GQ; ++h) sc[h] = 0.f;
 #pragma unroll
       for (int i = 0; i < DPT / 4; ++i) {
-        const float4 a = kr[i];
+        const int c = TPP * i + sub;
+        const float4 a = *(const float4*)(ks + p * KLD + 4 * c);
 #pragma unroll
         for (int h = 0; h < GQ; ++h) {
-          const float4 b = ((const float4*)(qs + h * HD + sub * DPT))[i];
+          const float4 b = *(const float4*)(qs + h * HD + 4 * c);
           sc[h] += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
         }
       }
@@ -907,14 +915,6 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
       if (sub == 0)
 #pragma unroll
         for (int h = 0; h < GQ; ++h) ps[h * C + p] = valid ? sc[h] * scale : -INFINITY;  // model.rs:397
-    }
-    if (k + 1 < nsub) {  // the next sub-tile's rows, in flight during this one's softmax and P.V
-      const size_t off = row_off(k + 1);
-#pragma unroll
-      for (int i = 0; i < DPT / 4; ++i) {
-        kr[i] = ((const float4*)(kc + off))[i];
-        vr[i] = ((const float4*)(vc + off))[i];
-      }
     }
     __syncthreads();
     for (int h = wv; h < GQ; h += 4) {  // C == 64: one wave per softmax row, running max and sum
