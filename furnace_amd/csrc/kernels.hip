@@ -578,21 +578,24 @@ __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
 size_t gemv_lds_bytes(uint32_t in, bool) { return (size_t)in * (in <= 4096 ? 8 : 4) + in / 4; }
 
 
-// Lanes per row: the choice in {16, 64} that keeps the most lanes busy
-// on real items, counting at most the 2048 waves that are resident at once
-// (ties: fewer lanes, so fewer blocks stage x).
-static int lanes_per_row(uint32_t total_rows, uint32_t type, int mode, int n_items) {
+// Lanes per row: the choice in {16, 32, 64} with the shortest critical
+// path, counted as the busiest wave's units times the steps of a unit, on
+// the waves that are resident at once (ties: fewer lanes, so fewer blocks
+// stage x).  E.g. the 1.5B SwiGLU pair (8960 rows of 48 items, 2 items per
+// lane and step): 16 lanes -> 2240 units of 2 steps on 2048 waves, 4
+// steps; 32 lanes -> 4480 units of 1 step, 3 steps.
+static uint32_t max_blocks(uint32_t in);
+static int lanes_per_row(uint32_t total_rows, uint32_t in, uint32_t type, int mode, int n_items) {
+  const uint32_t cap_waves = 4 * max_blocks(in);
   int best_l = 16;
-  double best_score = -1.0;
-  for (int l = 16; l <= 64; l *= 4) {
-    double waves = (double)total_rows * l / 64.0;
-    if (waves > 2048.0) waves = 2048.0;
-    int slots = l * gemv_bi(type, mode);
-    int steps = (n_items + slots - 1) / slots;
-    double eff = steps ? (double)n_items / ((double)slots * steps) : 0.0;
-    double score = waves * eff;
-    if (score > best_score * 1.05) {
-      best_score = score;
+  uint64_t best = ~0ull;
+  for (int l = 16; l <= 64; l *= 2) {
+    const uint32_t slots = (uint32_t)(l * gemv_bi(type, mode)), steps = ((uint32_t)n_items + slots - 1) / slots;
+    const uint32_t units = (total_rows + 64 / l - 1) / (64 / l);
+    const uint32_t waves = std::min(4 * ((units + 3) / 4), cap_waves);
+    const uint64_t cost = (uint64_t)((units + waves - 1) / waves) * steps;
+    if (cost < best) {
+      best = cost;
       best_l = l;
     }
   }
@@ -628,7 +631,7 @@ static uint32_t plan_blocks(GemvArgs& a, uint32_t rows_per_unit) {
 }
 
 uint32_t gemv_blocks(uint32_t type, uint32_t rows, uint32_t in) {
-  int lpr = lanes_per_row(rows, type, GEMV_STORE, items_per_row(type, in, ((in / 32) % 2) == 0));
+  int lpr = lanes_per_row(rows, in, type, GEMV_STORE, items_per_row(type, in, ((in / 32) % 2) == 0));
   uint32_t units = (rows + 64 / lpr - 1) / (64 / lpr), want = (units + 3) / 4, cap = max_blocks(in);
   return want < cap ? want : cap;
 }
@@ -660,8 +663,9 @@ template <uint32_t T0, uint32_t T1, int MODE>
 static hipError_t pick_lpr(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
   uint32_t rows = 0;
   for (int i = 0; i < a.n_seg; ++i) rows += a.seg[i].rows;
-  int lpr = lanes_per_row(rows, a.seg[0].type, MODE, items_per_row(a.seg[0].type, a.in, ((a.in / 32) % 2) == 0));
+  int lpr = lanes_per_row(rows, a.in, a.seg[0].type, MODE, items_per_row(a.seg[0].type, a.in, ((a.in / 32) % 2) == 0));
   if (lpr == 16) return pick_nx<T0, T1, MODE, 16>(a, s, nb);
+  if (lpr == 32) return pick_nx<T0, T1, MODE, 32>(a, s, nb);
   return pick_nx<T0, T1, MODE, 64>(a, s, nb);
 }
 
@@ -731,7 +735,7 @@ static hipError_t prep_one(int bytes) {
 template <uint32_t T0, uint32_t T1>
 static hipError_t prep_types(int bytes) {
   hipError_t e;
-  if ((e = prep_one<T0, T1, 16>(bytes))) return e;
+  if ((e = prep_one<T0, T1, 16>(bytes)) || (e = prep_one<T0, T1, 32>(bytes))) return e;
   return prep_one<T0, T1, 64>(bytes);
 }
 
