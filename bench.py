@@ -189,12 +189,15 @@ def main():
     tok = model.prefill(prompt)
     hip.sync()
     prefill_s = time.perf_counter() - t0
+    # the timed steps: frn_decode_greedy, the argmax fed back on the device
+    # and one host synchronisation per batch of steps
     hip.sync()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        tok = model.decode(tok)
+    ids = model.decode_greedy(tok, args.steps)
     hip.sync()
     dec_s = time.perf_counter() - t0
+    assert len(ids) == args.steps
+    tok = ids[-1]
     ms_per_step = dec_s * 1000.0 / args.steps
     # positions attended by the timed steps: prompt+1 .. prompt+steps
     avg_attended = args.prompt + (args.steps + 1) / 2.0
@@ -203,6 +206,19 @@ def main():
     log("decode: %d steps, %.4f ms/token, %.1f tokens/s, %.1f GB/s (%.1f%% of HBM peak)" %
         (args.steps, ms_per_step, 1000 / ms_per_step, step_gbs, 100 * step_gbs / HBM_PEAK_GBS))
     log("prefill: %d tokens in %.3f s (%.1f tokens/s)" % (args.prompt, prefill_s, args.prompt / prefill_s))
+    # the same steps through the one-step call (a host round trip per id)
+    model.reset()
+    tok = model.prefill(prompt)
+    hip.sync()
+    t0 = time.perf_counter()
+    loop_ids = []
+    for _ in range(args.steps):
+        tok = model.decode(tok)
+        loop_ids.append(tok)
+    hip.sync()
+    loop_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    assert loop_ids == ids, "frn_decode loop and frn_decode_greedy disagree"
+    log("decode, one frn_decode call per step: %.4f ms/token (%.1f tokens/s); same ids" % (loop_ms, 1000 / loop_ms))
 
     # live per-kernel durations (HIP events around each kernel, eager steps)
     model.timings_reset()
@@ -277,7 +293,9 @@ def main():
                    if "q4_k_m" in args.model else "Q8_0", "prompt_tokens": args.prompt,
                    "decode_tokens": args.steps, "bytes_per_token": int(step_bytes),
                    "hbm_frac_per_token": round(step_gbs / HBM_PEAK_GBS, 4),
-                   "prefill_tokens_per_s": round(args.prompt / prefill_s, 1)},
+                   "prefill_tokens_per_s": round(args.prompt / prefill_s, 1),
+                   "decode_api": "frn_decode_greedy (batches of 32 steps per host sync)",
+                   "per_call_decode_tokens_per_s": round(1000.0 / loop_ms, 1)},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": dk["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": dk["bytes"], "avg_us": dk["avg_us"]},

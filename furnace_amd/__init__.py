@@ -66,6 +66,7 @@ SIGNATURES = {
     "frn_finalize": (_I, [_P]),
     "frn_prefill": (_I, [_P, _P, _U32, ctypes.POINTER(_U32)]),
     "frn_decode": (_I, [_P, _U32, ctypes.POINTER(_U32)]),
+    "frn_decode_greedy": (_I, [_P, _U32, _U32, _P, _U32, _P, ctypes.POINTER(_U32)]),
     "frn_logits": (_I, [_P, _P, _SZ]),
     "frn_reset": (_I, [_P]),
     "frn_cache_len": (_I, [_P, ctypes.POINTER(_U32)]),
@@ -275,6 +276,18 @@ class Model:
         nxt = ctypes.c_uint32()
         check(load().frn_decode(self.ctx, int(tok), ctypes.byref(nxt)))
         return nxt.value
+
+    def decode_greedy(self, tok, n, stop_ids=()):
+        """n greedy steps from token tok (frn_decode_greedy): the ids of the
+        frn_decode loop, with one host synchronisation per batch of steps;
+        ends early after a step whose argmax is in stop_ids."""
+        out = np.zeros(max(int(n), 1), dtype=np.uint32)
+        stop = np.asarray(list(stop_ids), dtype=np.uint32)
+        done = ctypes.c_uint32()
+        check(load().frn_decode_greedy(self.ctx, int(tok), int(n),
+                                       stop.ctypes.data if len(stop) else None, len(stop),
+                                       out.ctypes.data, ctypes.byref(done)))
+        return [int(v) for v in out[:done.value]]
 
     def logits(self):
         out = np.empty(self.vocab, dtype=np.float32)

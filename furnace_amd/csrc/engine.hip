@@ -76,6 +76,8 @@ struct frn_ctx {
   uint32_t n_best = 0;
   StepState* st = nullptr;
   StepState* h_st = nullptr;  // pinned mirror for read-back
+  uint32_t* hist = nullptr;    // [max_ctx] argmax id of each decoded position (frn_decode_greedy)
+  uint32_t* h_hist = nullptr;  // pinned [GREEDY_BATCH] read-back of one batch
   // prefill rows: blocks of up to pf_rows prompt tokens through all layers
   uint32_t pf_rows = 0;
   float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_att = nullptr, *pf_act = nullptr,
@@ -102,10 +104,11 @@ static void free_ctx(frn_ctx* c) {
   if (c->graph_prefill) (void)hipGraphDestroy(c->graph_prefill);
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part, c->hist, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
+  if (c->h_hist) (void)hipHostFree(c->h_hist);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -117,6 +120,9 @@ static hipError_t dmalloc(T** p, size_t bytes) {
 
 // Prefill works on blocks of up to PREFILL_ROWS tokens (64-row GEMM tiles).
 constexpr uint32_t PREFILL_ROWS = 256;
+// frn_decode_greedy's steps per host synchronisation (and the most steps
+// that run past a stop id before the host sees it).
+constexpr uint32_t GREEDY_BATCH = 32;
 
 static hipError_t alloc_prefill(frn_ctx* x) {
   const frn_config& c = x->cfg;
@@ -171,6 +177,8 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
       (e = dmalloc(&x->rope, (size_t)c.max_ctx * c.head_dim * 4)) || (e = dmalloc(&x->st, sizeof(StepState))) ||
       (e = dmalloc(&x->best_part, ((size_t)c.vocab + 3) / 4 * 8)) ||  // >= lm_head blocks (4+ rows each)
       (e = alloc_prefill(x)) ||
+      (e = dmalloc(&x->hist, (size_t)c.max_ctx * 4)) ||
+      (e = hipHostMalloc((void**)&x->h_hist, GREEDY_BATCH * 4, hipHostMallocDefault)) ||
       (e = hipHostMalloc((void**)&x->h_st, sizeof(StepState), hipHostMallocDefault))) {
     free_ctx(x);
     return hip_fail(e, "frn_create: allocation");
@@ -379,7 +387,8 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
     lm.best = c->best_part;
     if (TIMED(CAT_LMHEAD, launch_gemv(lm, GEMV_ARGMAX, s, &c->n_best))) return e;
   }
-  TIMED(CAT_STEP, launch_step_end(c->st, with_logits ? c->best_part : nullptr, c->n_best, s));
+  TIMED(CAT_STEP, launch_step_end(c->st, with_logits ? c->best_part : nullptr, c->n_best,
+                                  with_logits ? c->hist : nullptr, s));
 #undef TIMED
   return e;
 }
@@ -466,9 +475,10 @@ extern "C" frn_status frn_finalize(frn_ctx* c) {
 }
 
 // Run one position with token `tok` (already validated); with_logits picks
-// the graph that ends in lm_head + argmax.
-static frn_status run_step(frn_ctx* c, uint32_t tok, bool with_logits) {
-  if (tok != c->last_next) {
+// the graph that ends in lm_head + argmax.  on_device: the token is the
+// previous step's argmax, already in StepState::tok.
+static frn_status run_step(frn_ctx* c, uint32_t tok, bool with_logits, bool on_device = false) {
+  if (!on_device && tok != c->last_next) {
     c->h_st->tok = tok;
     HIP_TRY(hipMemcpyAsync((char*)c->st + offsetof(StepState, tok), &c->h_st->tok, 4, hipMemcpyHostToDevice, c->stream),
             "token upload");
@@ -608,6 +618,62 @@ extern "C" frn_status frn_decode(frn_ctx* c, uint32_t id, uint32_t* next_id) {
   c->last_next = prev;  // run_step skips the upload when id is the device's own argmax
   if ((st = run_step(c, id, true))) return st;
   return read_next(c, next_id);
+}
+
+// Greedy decode without a host round trip per step (generate.rs:110-136 at
+// temperature 0): the step graphs go out back to back, each step's embed
+// reading the previous step's argmax from StepState::tok, and the host
+// reads one batch of ids (hist[pos], written by the step-end kernel) per
+// synchronisation.  A stop id ends the loop after the step that produced
+// it, as generate.rs:125-127 would; the position count is rolled back over
+// the steps of the batch that ran past it (their KV rows lie beyond the
+// cache length, where no later step reads before overwriting them).
+extern "C" frn_status frn_decode_greedy(frn_ctx* c, uint32_t id, uint32_t n, const uint32_t* stop_ids,
+                                        uint32_t n_stop, uint32_t* out_ids, uint32_t* n_done) {
+  frn_status st;
+  if (n_done) *n_done = 0;
+  if ((st = check_ready(c, n))) return st;
+  if (n && !out_ids) return fail(FRN_EINVAL, "frn_decode_greedy: null out_ids");
+  if (n_stop && !stop_ids) return fail(FRN_EINVAL, "frn_decode_greedy: null stop_ids");
+  if (id >= c->cfg.vocab) return fail(FRN_ETOKEN, "token id %u out of range (vocab %u)", id, c->cfg.vocab);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  uint32_t done = 0;
+  bool stopped = false, rolled = false;
+  while (done < n && !stopped) {
+    const uint32_t b = std::min<uint32_t>(n - done, GREEDY_BATCH), p0 = c->len;
+    for (uint32_t i = 0; i < b; ++i)
+      if ((st = run_step(c, id, true, done + i > 0))) return st;
+    HIP_TRY(hipMemcpyAsync(c->h_hist, c->hist + p0, (size_t)b * 4, hipMemcpyDeviceToHost, c->stream),
+            "id read-back");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    uint32_t used = b;
+    for (uint32_t i = 0; i < b && !stopped; ++i) {
+      out_ids[done + i] = c->h_hist[i];
+      for (uint32_t k = 0; k < n_stop; ++k)
+        if (c->h_hist[i] == stop_ids[k]) {
+          stopped = true;
+          used = i + 1;
+        }
+    }
+    done += used;
+    if (used < b) {  // roll the position back to just after the stop id's step
+      rolled = true;
+      c->len = p0 + used;
+      c->h_st->pos = c->len;
+      HIP_TRY(hipMemcpyAsync((char*)c->st + offsetof(StepState, pos), &c->h_st->pos, 4, hipMemcpyHostToDevice,
+                             c->stream),
+              "position roll-back");
+      HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    }
+  }
+  if (n_done) *n_done = done;
+  if (done) {
+    // the device's tok/next_tok hold the last step that ran; after a
+    // roll-back that is not the last one kept, so the next call uploads
+    c->last_next = rolled ? 0xFFFFFFFFu : out_ids[done - 1];
+    c->have_logits = !rolled;
+  }
+  return FRN_OK;
 }
 
 extern "C" frn_status frn_logits(frn_ctx* c, float* host_out, size_t n) {

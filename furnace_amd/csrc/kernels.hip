@@ -1013,7 +1013,7 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, cons
 // 1024 threads: max over the lm_head blocks' packed candidates (largest
 // logit, then smallest row), then advance the position.
 __global__ __launch_bounds__(1024) void k_step_end(StepState* st, const uint64_t* __restrict__ best,
-                                                   uint32_t n_best) {
+                                                   uint32_t n_best, uint32_t* __restrict__ hist) {
   __shared__ uint64_t wb[16];
   if (best) {
     uint64_t b = 0;
@@ -1029,13 +1029,14 @@ __global__ __launch_bounds__(1024) void k_step_end(StepState* st, const uint64_t
       uint32_t idx = 0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull);
       st->next_tok = idx;
       st->tok = idx;
+      if (hist) hist[st->pos] = idx;
     }
   }
   if (threadIdx.x == 0) st->pos += 1;
 }
 
-hipError_t launch_step_end(StepState* st, const uint64_t* best, uint32_t n_best, hipStream_t s) {
-  hipLaunchKernelGGL(k_step_end, dim3(1), dim3(1024), 0, s, st, best, n_best);
+hipError_t launch_step_end(StepState* st, const uint64_t* best, uint32_t n_best, uint32_t* hist, hipStream_t s) {
+  hipLaunchKernelGGL(k_step_end, dim3(1), dim3(1024), 0, s, st, best, n_best, hist);
   return hipGetLastError();
 }
 

@@ -80,8 +80,9 @@ __host__ __device__ inline uint32_t attention_split_len(uint32_t T) {
 // heads per kv head.
 bool attention_supported(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
 // Ends a step: reduces the lm_head kernel's per-block argmax candidates
-// (best == nullptr for a step without logits) and advances the position.
-hipError_t launch_step_end(StepState* st, const uint64_t* best, uint32_t n_best, hipStream_t s);
+// (best == nullptr for a step without logits) into next_tok/tok, records
+// the id at hist[pos] when hist is given, and advances the position.
+hipError_t launch_step_end(StepState* st, const uint64_t* best, uint32_t n_best, uint32_t* hist, hipStream_t s);
 hipError_t launch_argmax(const float* x, size_t n, uint64_t* scratch, uint32_t* out, hipStream_t s);
 
 // ---- prefill (prefill.hip) ----------------------------------------------------

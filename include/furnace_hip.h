@@ -94,6 +94,19 @@ frn_status frn_prefill(frn_ctx* ctx, const uint32_t* ids, uint32_t n, uint32_t* 
  * (generate.rs:136, :124).  Only the next id crosses back to the host. */
 frn_status frn_decode(frn_ctx* ctx, uint32_t id, uint32_t* next_id);
 
+/* Greedy decode of up to n steps (the loop of generate.rs:110-136 at
+ * temperature 0, as n frn_decode calls where each feeds back the previous
+ * next_id): step i runs at position ctx.len and decodes `id` (i = 0) or
+ * out_ids[i-1], writing its argmax to out_ids[i].  The steps are enqueued
+ * back to back, the argmax feeding the next step on the device, and the
+ * host synchronises once per batch of up to 32 steps.  If out_ids[i] is one
+ * of the n_stop stop_ids, the loop ends there (generate.rs:125-127) with
+ * *n_done = i + 1 and ctx.len just past step i; steps of the batch that ran
+ * beyond it are rolled back and frn_logits has nothing to return.  The ids
+ * equal those of the frn_decode loop. */
+frn_status frn_decode_greedy(frn_ctx* ctx, uint32_t id, uint32_t n, const uint32_t* stop_ids, uint32_t n_stop,
+                             uint32_t* out_ids, uint32_t* n_done);
+
 /* Copy the last step's logits [vocab] to host memory (the 1e-3 parity gate
  * and any host-side sampler).  n must be >= vocab. */
 frn_status frn_logits(frn_ctx* ctx, float* host_out, size_t n);

@@ -52,6 +52,7 @@ def test_context_calls_reject_null():
     lib = fa.load()
     nxt = ctypes.c_uint32()
     assert lib.frn_decode(None, 0, ctypes.byref(nxt)) == 1
+    assert lib.frn_decode_greedy(None, 0, 4, None, 0, None, ctypes.byref(nxt)) == 1
     assert lib.frn_prefill(None, None, 0, ctypes.byref(nxt)) == 1
     assert lib.frn_finalize(None) == 1
     assert lib.frn_reset(None) == 1
