@@ -25,6 +25,46 @@ namespace frn {
 
 enum : uint32_t { T_F32 = 0, T_Q5_0 = 6, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
 
+// ---- cross-lane all-reduce ----------------------------------------------------
+// All-reduce over aligned groups of W lanes (W a power of two up to 64):
+// DPP moves inside each 16-lane row (quad xor 1, quad xor 2, half-row
+// mirror, row mirror -- every lane ends with its group's result, paired as
+// in an xor butterfly) and v_readlane across rows.  __shfl_xor compiles to
+// ds_bpermute, a round trip through the LDS crossbar per step; a DPP move
+// is an operand modifier of the VALU instruction.  Every lane of the wave
+// must be active.
+template <int CTRL, class T>
+__device__ __forceinline__ T dpp_mov(T v) {
+  return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <class T>
+__device__ __forceinline__ T lane_read(T v, int lane) {
+  return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+struct OpAdd {
+  template <class T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct OpMax {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+template <int W, class T, class Op = OpAdd>
+__device__ __forceinline__ T group_reduce(T v, Op op = Op()) {
+  static_assert(sizeof(T) == 4 && W >= 1 && W <= 64 && (W & (W - 1)) == 0, "32-bit values, W = 2^k <= 64");
+  if constexpr (W >= 2) v = op(v, dpp_mov<0xB1>(v));    // quad_perm [1,0,3,2]
+  if constexpr (W >= 4) v = op(v, dpp_mov<0x4E>(v));    // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) v = op(v, dpp_mov<0x141>(v));   // row_half_mirror
+  if constexpr (W >= 16) v = op(v, dpp_mov<0x140>(v));  // row_mirror
+  if constexpr (W >= 32) {
+    const T r0 = lane_read(v, 0), r1 = lane_read(v, 16), r2 = lane_read(v, 32), r3 = lane_read(v, 48);
+    if constexpr (W == 64)
+      v = op(op(r0, r1), op(r2, r3));
+    else
+      v = (__lane_id() & 32) ? op(r2, r3) : op(r0, r1);
+  }
+  return v;
+}
+
 __host__ __device__ constexpr int blk_elems(uint32_t t) {
   return t == T_Q4_K || t == T_Q6_K ? 256 : (t == T_F32 ? 1 : 32);
 }

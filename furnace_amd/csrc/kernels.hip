@@ -14,16 +14,8 @@ uint32_t attention_splits(uint32_t max_ctx) {
 }
 
 // ---- reductions -----------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return group_reduce<64>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_reduce<64>(v, OpMax()); }
 // Sum over a 256-thread block; every thread gets the result.
 __device__ __forceinline__ float block_sum256(float v, float* red4) {
   v = wave_sum(v);
@@ -302,7 +294,7 @@ struct XStage {
       }
       if (!DIG) {
         float s16 = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
-        s16 += __shfl_xor(s16, 1, 2);
+        s16 = group_reduce<2>(s16);
         if (live && (u & 1) == 0) ((float*)pl)[u >> 1] = s16;
         continue;
       }
@@ -313,8 +305,7 @@ struct XStage {
         amax = fmaxf(amax, fabsf(v[j]));
         xsum += v[j];
       }
-      amax = fmaxf(amax, __shfl_xor(amax, 1, 4));
-      amax = fmaxf(amax, __shfl_xor(amax, 2, 4));  // over the 32-value chunk
+      amax = group_reduce<4>(amax, OpMax());  // over the 32-value chunk
       const float inv_s = amax > 0.f ? 127.0f / amax : 0.f;
       const float cs = amax > 0.f ? (1.0f / inv_s) * (1.0f / 16384.0f) : 0.f;
       uint32_t w0[2] = {0, 0}, w1[2] = {0, 0}, w2[2] = {0, 0};
@@ -334,10 +325,10 @@ struct XStage {
         s2 += d2;
       }
       // per 16-value record: the two threads u, u^1
-      xsum += __shfl_xor(xsum, 1, 2);
-      s0 += __shfl_xor(s0, 1, 2);
-      s1 += __shfl_xor(s1, 1, 2);
-      s2 += __shfl_xor(s2, 1, 2);
+      xsum = group_reduce<2>(xsum);
+      s0 = group_reduce<2>(s0);
+      s1 = group_reduce<2>(s1);
+      s2 = group_reduce<2>(s2);
       if (live) {
         const uint32_t c = u >> 1, off = 16u * swz(c, n16) + 8u * (u & 1);
         *(uint2*)(pl + off) = make_uint2(w0[0], w0[1]);
@@ -451,12 +442,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
       }
     }
     if (step + 1 < S) return;
-    float acc0 = acc[0], acc1 = acc[R - 1];
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) {
-      acc0 += __shfl_xor(acc0, o, LPR);
-      if (MODE == GEMV_SWIGLU) acc1 += __shfl_xor(acc1, o, LPR);
-    }
+    const float acc0 = group_reduce<LPR>(acc[0]), acc1 = MODE == GEMV_SWIGLU ? group_reduce<LPR>(acc[R - 1]) : 0.f;
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.f;
     if (gl == 0 && row < sg.rows) {
@@ -913,9 +899,7 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
         }
       }
 #pragma unroll
-      for (int o = TPP / 2; o > 0; o >>= 1)
-#pragma unroll
-        for (int h = 0; h < GQ; ++h) sc[h] += __shfl_xor(sc[h], o, TPP);
+      for (int h = 0; h < GQ; ++h) sc[h] = group_reduce<TPP>(sc[h]);
       if (sub == 0)
 #pragma unroll
         for (int h = 0; h < GQ; ++h) ps[h * C + p] = valid ? sc[h] * scale : -INFINITY;  // model.rs:397

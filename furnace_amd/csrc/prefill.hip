@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void k_row_inv(const float* __restrict__ x, ui
   const float* row = x + (size_t)blockIdx.x * cols;
   float ss = 0.f;
   for (uint32_t i = threadIdx.x; i < cols; i += 256) ss += row[i] * row[i];
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  ss = group_reduce<64>(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   if (threadIdx.x == 0) inv[blockIdx.x] = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)cols + eps);
@@ -381,8 +381,7 @@ __global__ __launch_bounds__(256) void k_attn_rows(const float* __restrict__ q, 
       float s = 0.f;
 #pragma unroll
       for (int d = 0; d < DS; ++d) s = fmaf(qv[d], Ks[j * (HD + 1) + sub * DS + d], s);
-      s += __shfl_xor(s, 1, 4);
-      s += __shfl_xor(s, 2, 4);
+      s = group_reduce<4>(s);
       sc[j] = (k0 + j <= qpos) ? s * scale : -INFINITY;  // model.rs:397, causal mask
     }
     float mt = m;
