@@ -17,7 +17,8 @@ LIB = os.path.join(PKG, "lib", "libfurnace_hip.so")
 CLI = os.path.join(PKG, "bin", "furnace-hip")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-# packed-fp32 instructions are disabled for all device code
+# packed-fp32 instructions are disabled for all device code: some of their
+# forms have given wrong results on this hardware
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",

@@ -160,7 +160,7 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
   hipDeviceProp_t prop;
   HIP_TRY(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
-    return fail(FRN_ENODEV, "frn_create: device %d is %s, this build targets gfx950", device, prop.gcnArchName);
+    return fail(FRN_ENODEV, "frn_create: device %d is %s, this library targets gfx950", device, prop.gcnArchName);
   frn_ctx* x = new frn_ctx();
   x->cfg = c;
   x->device = device;

@@ -1,4 +1,4 @@
-/* Test infrastructure only (the checker).  Restates src/gguf.rs parse /
+/* Test infrastructure only (the oracle).  Restates src/gguf.rs parse /
  * open / tensor: bounds-checked reads over an mmap, metadata values, tensor
  * table, data blob at the next multiple of general.alignment (default 32). */
 #include <fcntl.h>

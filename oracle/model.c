@@ -1,4 +1,4 @@
-/* Test infrastructure only (the checker).  Restates src/model.rs (Config,
+/* Test infrastructure only (the oracle).  Restates src/model.rs (Config,
  * Weight, Layer, linear, KvCache, layer_forward[_cached], embed, Model::load,
  * forward_cached, forward_last, last_row_logits) and the temperature-0 path
  * of src/generate.rs::generate. */

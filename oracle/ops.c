@@ -1,4 +1,4 @@
-/* Test infrastructure only (the checker).  Restates the f32 ops of furnace's
+/* Test infrastructure only (the oracle).  Restates the f32 ops of furnace's
  * src/tensor.rs and the position/attention ops of src/model.rs. */
 #include <math.h>
 #include <string.h>

@@ -1,6 +1,6 @@
 /*
  * oracle.h -- CPU restatement of furnace's token loop, used ONLY as the
- * checker: tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * test oracle: tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
  * load it.  The product (furnace_amd/) never links, loads or calls it.
  *
  * Every function restates one reference function and cites it (paths are

@@ -1,7 +1,7 @@
 """ctypes view of oracle/liboracle.so -- test infrastructure only.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
-this module, as the checker.  The product (furnace_amd/) never does.
+this module, as the test oracle.  The product (furnace_amd/) never does.
 """
 import ctypes
 import os

@@ -1,4 +1,4 @@
-/* Test infrastructure only (the checker).  Restates src/quant.rs of furnace.
+/* Test infrastructure only (the oracle).  Restates src/quant.rs of furnace.
  * Built with -ffp-contract=off: every product and sum rounds separately, as
  * Rust's f32 arithmetic does. */
 #include <math.h>

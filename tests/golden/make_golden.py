@@ -38,7 +38,7 @@ GEMV_SHAPES = [("q4_k", 8960, 1536), ("q4_k", 1536, 8960), ("q6_k", 1536, 8960),
 GEMV_ROWS = 16
 TINY = dict(n_layers=2, n_heads=4, n_kv_heads=2, hidden=256, ffn=512, vocab=1000, mix=fa.MIX_Q4_K_M, tied=1,
             embd_type=fa.Q6_K, output_type=fa.Q6_K)
-TINY_SEED, CFG1_SEED = 23, 0xF0E1 + 1
+TINY_SEED, Q8_05B_SEED = 23, 0xF0E1 + 1
 
 
 def sha256(path):
@@ -100,7 +100,7 @@ def main():
     dequant()
     gemv()
     model_fixture("tiny.npz", TINY, TINY_SEED, 12, 64)
-    model_fixture("qwen2-0.5b-q8_0.npz", fa.PRESETS["qwen2-0.5b-q8_0"], CFG1_SEED, 16, 64)
+    model_fixture("qwen2-0.5b-q8_0.npz", fa.PRESETS["qwen2-0.5b-q8_0"], Q8_05B_SEED, 16, 64)
 
 
 if __name__ == "__main__":

@@ -83,7 +83,7 @@ def test_create_without_device_reports_enodev():
 
 
 def test_product_path_does_not_touch_the_oracle():
-    # the product package must never load or mention the checker
+    # the product package must never load or mention the oracle
     pkg = os.path.join(ROOT, "furnace_amd")
     for dirpath, _, files in os.walk(pkg):
         for f in files:
