@@ -67,6 +67,9 @@ SIGNATURES = {
     "frn_prefill": (_I, [_P, _P, _U32, ctypes.POINTER(_U32)]),
     "frn_decode": (_I, [_P, _U32, ctypes.POINTER(_U32)]),
     "frn_decode_greedy": (_I, [_P, _U32, _U32, _P, _U32, _P, ctypes.POINTER(_U32)]),
+    "frn_sampler_init": (_I, [_P, ctypes.c_float, _U32, ctypes.c_float, ctypes.c_float, ctypes.c_uint64]),
+    "frn_sample": (_I, [_P, _P, _U32, ctypes.POINTER(_U32)]),
+    "frn_sampler_draws": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
     "frn_logits": (_I, [_P, _P, _SZ]),
     "frn_reset": (_I, [_P]),
     "frn_cache_len": (_I, [_P, ctypes.POINTER(_U32)]),
@@ -288,6 +291,23 @@ class Model:
                                        stop.ctypes.data if len(stop) else None, len(stop),
                                        out.ctypes.data, ctypes.byref(done)))
         return [int(v) for v in out[:done.value]]
+
+    def sampler_init(self, temperature, top_k, top_p, repeat_penalty=1.0, seed=7):
+        """Sampler::new on the device (frn_sampler_init)."""
+        check(load().frn_sampler_init(self.ctx, float(temperature), int(top_k), float(top_p),
+                                      float(repeat_penalty), int(seed)))
+
+    def sample(self, recent=()):
+        """Sampler::sample on the last step's device logits (frn_sample)."""
+        r = np.ascontiguousarray(list(recent), dtype=np.uint32)
+        nxt = ctypes.c_uint32()
+        check(load().frn_sample(self.ctx, r.ctypes.data if r.size else None, r.size, ctypes.byref(nxt)))
+        return nxt.value
+
+    def sampler_draws(self):
+        d = ctypes.c_uint64()
+        check(load().frn_sampler_draws(self.ctx, ctypes.byref(d)))
+        return d.value
 
     def logits(self):
         out = np.empty(self.vocab, dtype=np.float32)

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <map>
 #include <string>
 #include <vector>
@@ -20,6 +21,7 @@
 #include "common.hpp"
 #include "formats.hpp"
 #include "kernels.hpp"
+#include "sampler.hpp"
 
 using namespace frn;
 
@@ -78,6 +80,15 @@ struct frn_ctx {
   StepState* h_st = nullptr;  // pinned mirror for read-back
   uint32_t* hist = nullptr;    // [max_ctx] argmax id of each decoded position (frn_decode_greedy)
   uint32_t* h_hist = nullptr;  // pinned [GREEDY_BATCH] read-back of one batch
+  // device sampler (frn_sampler_init / frn_sample)
+  SamplerRng* rng = nullptr;                           // Pcg32 state and draw count
+  float* cand_v = nullptr;                             // per-block candidates
+  uint32_t *cand_id = nullptr, *recent = nullptr;      // [SAMPLER_MAX_RECENT] recent ids
+  uint32_t* h_recent = nullptr;                        // pinned staging of the recent ids
+  SamplerRng* h_rng = nullptr;                         // pinned staging of the RNG state
+  bool sampler_ready = false;
+  float s_temperature = 0.f, s_top_p = 1.f, s_penalty = 1.f;
+  uint32_t s_top_k = 0;
   // prefill rows: blocks of up to pf_rows prompt tokens through all layers
   uint32_t pf_rows = 0;
   float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_att = nullptr, *pf_act = nullptr,
@@ -104,11 +115,13 @@ static void free_ctx(frn_ctx* c) {
   if (c->graph_prefill) (void)hipGraphDestroy(c->graph_prefill);
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part, c->hist, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part, c->hist, c->rng, c->cand_v, c->cand_id, c->recent, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
   if (c->h_hist) (void)hipHostFree(c->h_hist);
+  if (c->h_recent) (void)hipHostFree(c->h_recent);
+  if (c->h_rng) (void)hipHostFree(c->h_rng);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -179,6 +192,12 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
       (e = alloc_prefill(x)) ||
       (e = dmalloc(&x->hist, (size_t)c.max_ctx * 4)) ||
       (e = hipHostMalloc((void**)&x->h_hist, GREEDY_BATCH * 4, hipHostMallocDefault)) ||
+      (e = dmalloc(&x->rng, sizeof(SamplerRng))) ||
+      (e = dmalloc(&x->cand_v, (size_t)sampler_blocks(c.vocab) * SAMPLER_MAX_K * 4)) ||
+      (e = dmalloc(&x->cand_id, (size_t)sampler_blocks(c.vocab) * SAMPLER_MAX_K * 4)) ||
+      (e = dmalloc(&x->recent, SAMPLER_MAX_RECENT * 4)) ||
+      (e = hipHostMalloc((void**)&x->h_recent, SAMPLER_MAX_RECENT * 4, hipHostMallocDefault)) ||
+      (e = hipHostMalloc((void**)&x->h_rng, sizeof(SamplerRng), hipHostMallocDefault)) ||
       (e = hipHostMalloc((void**)&x->h_st, sizeof(StepState), hipHostMallocDefault))) {
     free_ctx(x);
     return hip_fail(e, "frn_create: allocation");
@@ -683,6 +702,87 @@ extern "C" frn_status frn_logits(frn_ctx* c, float* host_out, size_t n) {
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
   HIP_TRY(hipMemcpyAsync(host_out, c->logits, (size_t)c->cfg.vocab * 4, hipMemcpyDeviceToHost, c->stream), "logits copy");
   HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return FRN_OK;
+}
+
+// ---- sampler (sampler.rs) -----------------------------------------------------
+// Pcg32::new(seed) (sampler.rs:11-17) on the host: O'Neill's
+// pcg32_srandom_r with initstate = seed, initseq = 0xda3e39cb94b95bdb.
+static uint32_t pcg32_step(SamplerRng& r) {
+  const uint64_t old = r.state;
+  r.state = old * 6364136223846793005ull + r.inc;
+  const uint32_t xs = (uint32_t)(((old >> 18) ^ old) >> 27), rot = (uint32_t)(old >> 59);
+  return (xs >> rot) | (xs << ((32u - rot) & 31u));
+}
+
+extern "C" frn_status frn_sampler_init(frn_ctx* c, float temperature, uint32_t top_k, float top_p,
+                                       float repeat_penalty, uint64_t seed) {
+  if (!c) return fail(FRN_EINVAL, "frn_sampler_init: null context");
+  if (!c->finalized) return fail(FRN_EINVAL, "frn_sampler_init: context not finalized");
+  if (!(temperature >= 0.0f) || !std::isfinite(temperature))
+    return fail(FRN_EINVAL, "frn_sampler_init: temperature %g must be finite and >= 0", (double)temperature);
+  if (!std::isfinite(top_p)) return fail(FRN_EINVAL, "frn_sampler_init: top_p must be finite");
+  if (!(repeat_penalty > 0.0f) || !std::isfinite(repeat_penalty))
+    return fail(FRN_EINVAL, "frn_sampler_init: repeat_penalty %g must be finite and > 0", (double)repeat_penalty);
+  const bool draw = !(temperature == 0.0f || top_k == 1);
+  if (draw && (top_k == 0 || top_k > SAMPLER_MAX_K))
+    return fail(FRN_EINVAL, "frn_sampler_init: the device sampler takes top_k 1..%u (got %u; 0 = no cut is not supported)",
+                SAMPLER_MAX_K, top_k);
+  if (sampler_sort_size(c->cfg.vocab, draw ? top_k : 1) > SAMPLER_MAX_SORT)
+    return fail(FRN_EINVAL, "frn_sampler_init: vocab %u x top_k %u candidates exceed the %u the sampler sorts",
+                c->cfg.vocab, top_k, SAMPLER_MAX_SORT);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  HIP_TRY(sampler_prepare(c->cfg.vocab, SAMPLER_MAX_K), "sampler LDS limit");
+  SamplerRng r{0, (0xda3e39cb94b95bdbull << 1) | 1u, 0};
+  pcg32_step(r);
+  r.state += seed;
+  pcg32_step(r);
+  *c->h_rng = r;
+  HIP_TRY(hipMemcpyAsync(c->rng, c->h_rng, sizeof r, hipMemcpyHostToDevice, c->stream), "sampler state upload");
+  HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  c->s_temperature = temperature;
+  c->s_top_k = top_k;
+  c->s_top_p = top_p;
+  c->s_penalty = repeat_penalty;
+  c->sampler_ready = true;
+  return FRN_OK;
+}
+
+// Sampler::sample (sampler.rs:86-108) on the device logits of the last
+// frn_prefill / frn_decode step; the id also becomes the device's next
+// token, so a following frn_decode(ctx, id) uploads nothing.
+extern "C" frn_status frn_sample(frn_ctx* c, const uint32_t* recent, uint32_t n_recent, uint32_t* next_id) {
+  if (!c) return fail(FRN_EINVAL, "frn_sample: null context");
+  if (!c->sampler_ready) return fail(FRN_EINVAL, "frn_sample: call frn_sampler_init first");
+  if (!c->have_logits) return fail(FRN_EINVAL, "frn_sample: no logits yet");
+  if (n_recent > SAMPLER_MAX_RECENT)
+    return fail(FRN_EINVAL, "frn_sample: %u recent ids exceed %u", n_recent, SAMPLER_MAX_RECENT);
+  if (n_recent && !recent) return fail(FRN_EINVAL, "frn_sample: null recent ids");
+  for (uint32_t i = 0; i < n_recent; ++i)
+    if (recent[i] >= c->cfg.vocab) return fail(FRN_ETOKEN, "frn_sample: recent id %u out of range", recent[i]);
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  const bool draw = !(c->s_temperature == 0.0f || c->s_top_k == 1);
+  if (n_recent) {
+    memcpy(c->h_recent, recent, (size_t)n_recent * 4);
+    HIP_TRY(hipMemcpyAsync(c->recent, c->h_recent, (size_t)n_recent * 4, hipMemcpyHostToDevice, c->stream),
+            "recent ids upload");
+  }
+  HIP_TRY(launch_sample(c->logits, c->cfg.vocab, c->recent, n_recent, c->s_penalty,
+                        draw ? c->s_temperature : 1.0f, draw ? std::min(c->s_top_k, SAMPLER_MAX_K) : 1u,
+                        c->s_top_p, draw, c->cand_v, c->cand_id, c->rng, c->st, c->stream),
+          "sampler launch");
+  frn_status st = read_next(c, next_id);
+  // the host buffer is reused by the next call: the copy above has run
+  return st;
+}
+
+extern "C" frn_status frn_sampler_draws(frn_ctx* c, uint64_t* draws) {
+  if (!c || !draws) return fail(FRN_EINVAL, "frn_sampler_draws: null argument");
+  if (!c->sampler_ready) return fail(FRN_EINVAL, "frn_sampler_draws: call frn_sampler_init first");
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  HIP_TRY(hipMemcpyAsync(c->h_rng, c->rng, sizeof(SamplerRng), hipMemcpyDeviceToHost, c->stream), "draws read-back");
+  HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  *draws = c->h_rng->draws;
   return FRN_OK;
 }
 

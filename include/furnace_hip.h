@@ -107,6 +107,28 @@ frn_status frn_decode(frn_ctx* ctx, uint32_t id, uint32_t* next_id);
 frn_status frn_decode_greedy(frn_ctx* ctx, uint32_t id, uint32_t n, const uint32_t* stop_ids, uint32_t n_stop,
                              uint32_t* out_ids, uint32_t* n_done);
 
+/* Sampler::new (sampler.rs:68-78) on the device: temperature, top_k, top_p,
+ * repeat penalty (1.0 disables) and the PCG32 seed (Pcg32::new).  At
+ * temperature 0 or top_k 1, frn_sample is the argmax of the penalized logits
+ * and takes no RNG draw (sampler.rs:91-94).  Otherwise top_k must be 1..64:
+ * the reference's top_k 0 ("no cut") is not supported on the device and is
+ * rejected (FRN_EINVAL). */
+frn_status frn_sampler_init(frn_ctx* ctx, float temperature, uint32_t top_k, float top_p, float repeat_penalty,
+                            uint64_t seed);
+
+/* Sampler::sample(logits, recent) (sampler.rs:86-108) on the device logits of
+ * the last frn_prefill / frn_decode: repeat penalty over the unique ids of
+ * recent[0..n_recent) (generate.rs:123 passes the last repeat_window = 64
+ * context ids; at most 256), temperature, top-k, softmax, top-p, renormalize,
+ * one PCG32 draw.  The id also becomes the device's next token, so
+ * frn_decode(ctx, *next_id) uploads nothing.  Equal scaled logits are taken
+ * in ascending id order (the reference's unstable sort leaves them
+ * unordered). */
+frn_status frn_sample(frn_ctx* ctx, const uint32_t* recent, uint32_t n_recent, uint32_t* next_id);
+
+/* Sampler::draws (sampler.rs:82-84): RNG draws taken since frn_sampler_init. */
+frn_status frn_sampler_draws(frn_ctx* ctx, uint64_t* draws);
+
 /* Copy the last step's logits [vocab] to host memory (the 1e-3 parity gate
  * and any host-side sampler).  n must be >= vocab. */
 frn_status frn_logits(frn_ctx* ctx, float* host_out, size_t n);

@@ -65,6 +65,32 @@ void orc_attention_apply(const float* probs, const float* v, size_t seq, size_t 
 /* ---- generate.rs ------------------------------------------------------- */
 uint32_t orc_argmax(const float* x, size_t n); /* :69-77 */
 
+/* ---- sampler.rs --------------------------------------------------------- */
+typedef struct orc_pcg32 {
+  uint64_t state, inc;
+} orc_pcg32;
+/* O'Neill's pcg32_srandom_r; Pcg32::new(seed) = (seed, 0xda3e39cb94b95bdb) (:11-17) */
+void orc_pcg32_seed(orc_pcg32* r, uint64_t initstate, uint64_t initseq);
+uint32_t orc_pcg32_next_u32(orc_pcg32* r); /* :20-28 */
+float orc_pcg32_next_f32(orc_pcg32* r);    /* :31-33 */
+void orc_apply_repeat_penalty(float* logits, const uint32_t* recent, size_t n_recent, float penalty); /* :39-55 */
+typedef struct orc_sampler {               /* Sampler (:57-66) */
+  float temperature;
+  uint32_t top_k; /* 0 disables the cut */
+  float top_p;    /* 1.0 disables the cut */
+  float repeat_penalty;
+  uint32_t repeat_window;
+  orc_pcg32 rng;
+  uint64_t draws;
+} orc_sampler;
+void orc_sampler_new(orc_sampler* s, float temperature, uint32_t top_k, float top_p, float repeat_penalty,
+                     uint64_t seed); /* :68-78 */
+/* :117-155: (id, prob) by descending prob into ids/probs (room for n); returns the count */
+size_t orc_sampler_filtered(const orc_sampler* s, const float* logits, size_t n, uint32_t* ids, float* probs);
+/* :86-108 */
+uint32_t orc_sampler_sample(orc_sampler* s, const float* logits, size_t n, const uint32_t* recent,
+                            size_t n_recent);
+
 /* ---- GGUF (gguf.rs) and model (model.rs) -------------------------------- */
 typedef struct orc_config {            /* model.rs:26-38 */
   uint32_t n_layers, n_heads, n_kv_heads, hidden, ffn, head_dim, vocab, context_length;

@@ -26,8 +26,25 @@ class F32Layer(ctypes.Structure):
                 ("attn_norm", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "ffn_norm", "w_gate", "w_up", "w_down")]
 
 
+class Pcg32State(ctypes.Structure):
+    _fields_ = [("state", ctypes.c_uint64), ("inc", ctypes.c_uint64)]
+
+
+class SamplerState(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_uint32), ("top_p", ctypes.c_float),
+                ("repeat_penalty", ctypes.c_float), ("repeat_window", ctypes.c_uint32), ("rng", Pcg32State),
+                ("draws", ctypes.c_uint64)]
+
+
 _P, _SZ, _U32, _F = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_float
 _SIG = {
+    "orc_pcg32_seed": (None, [ctypes.POINTER(Pcg32State), ctypes.c_uint64, ctypes.c_uint64]),
+    "orc_pcg32_next_u32": (_U32, [ctypes.POINTER(Pcg32State)]),
+    "orc_pcg32_next_f32": (_F, [ctypes.POINTER(Pcg32State)]),
+    "orc_apply_repeat_penalty": (None, [_P, _P, _SZ, _F]),
+    "orc_sampler_new": (None, [ctypes.POINTER(SamplerState), _F, _U32, _F, _F, ctypes.c_uint64]),
+    "orc_sampler_filtered": (_SZ, [ctypes.POINTER(SamplerState), _P, _SZ, _P, _P]),
+    "orc_sampler_sample": (_U32, [ctypes.POINTER(SamplerState), _P, _SZ, _P, _SZ]),
     "orc_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
     "orc_dequantize": (ctypes.c_int, [_U32, _P, _SZ, _SZ, _P]),
     "orc_matmul_quant": (ctypes.c_int, [_P, _SZ, _P, _SZ, _SZ, _SZ, _U32, _P]),
@@ -179,6 +196,53 @@ def attention_apply(probs, v, n_heads, n_kv_heads, head_dim):
     out = np.empty((seq, n_heads * head_dim), dtype=np.float32)
     lib().orc_attention_apply(_p(probs), _p(v), seq, n_heads, n_kv_heads, head_dim, _p(out))
     return out
+
+
+class Pcg32:
+    """Pcg32 (sampler.rs:5-35); seed(initstate, initseq) is O'Neill's
+    pcg32_srandom_r, and Pcg32(seed) the reference's Pcg32::new(seed)."""
+
+    def __init__(self, seed=None, initseq=0xda3e39cb94b95bdb):
+        self.st = Pcg32State()
+        if seed is not None:
+            lib().orc_pcg32_seed(ctypes.byref(self.st), seed, initseq)
+
+    def next_u32(self):
+        return lib().orc_pcg32_next_u32(ctypes.byref(self.st))
+
+    def next_f32(self):
+        return lib().orc_pcg32_next_f32(ctypes.byref(self.st))
+
+
+def apply_repeat_penalty(logits, recent, penalty):
+    x = f32(logits).copy()
+    r = np.ascontiguousarray(recent, dtype=np.uint32)
+    lib().orc_apply_repeat_penalty(_p(x), _p(r) if r.size else None, r.size, penalty)
+    return x
+
+
+class Sampler:
+    """Sampler (sampler.rs:57-155)."""
+
+    def __init__(self, temperature, top_k, top_p, repeat_penalty=1.0, seed=7):
+        self.st = SamplerState()
+        lib().orc_sampler_new(ctypes.byref(self.st), temperature, top_k, top_p, repeat_penalty, seed)
+
+    @property
+    def draws(self):
+        return self.st.draws
+
+    def filtered(self, logits):
+        x = f32(logits)
+        ids = np.empty(x.size, dtype=np.uint32)
+        pr = np.empty(x.size, dtype=np.float32)
+        n = lib().orc_sampler_filtered(ctypes.byref(self.st), _p(x), x.size, _p(ids), _p(pr))
+        return ids[:n], pr[:n]
+
+    def sample(self, logits, recent=()):
+        x = f32(logits)
+        r = np.ascontiguousarray(recent, dtype=np.uint32)
+        return int(lib().orc_sampler_sample(ctypes.byref(self.st), _p(x), x.size, _p(r) if r.size else None, r.size))
 
 
 def argmax(x):

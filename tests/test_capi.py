@@ -53,6 +53,9 @@ def test_context_calls_reject_null():
     nxt = ctypes.c_uint32()
     assert lib.frn_decode(None, 0, ctypes.byref(nxt)) == 1
     assert lib.frn_decode_greedy(None, 0, 4, None, 0, None, ctypes.byref(nxt)) == 1
+    assert lib.frn_sampler_init(None, 0.7, 40, 0.9, 1.0, 7) == 1
+    assert lib.frn_sample(None, None, 0, ctypes.byref(nxt)) == 1
+    assert lib.frn_sampler_draws(None, None) == 1
     assert lib.frn_prefill(None, None, 0, ctypes.byref(nxt)) == 1
     assert lib.frn_finalize(None) == 1
     assert lib.frn_reset(None) == 1
