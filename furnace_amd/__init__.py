@@ -91,6 +91,9 @@ SIGNATURES = {
                              ctypes.POINTER(_U32), ctypes.POINTER(_P), ctypes.POINTER(_SZ)]),
     "frn_model_load": (_I, [_P, _I, _U32, _U32, ctypes.POINTER(_P)]),
     "frn_generate_greedy": (_I, [_P, _P, _U32, _U32, _P, _U32, _P, ctypes.POINTER(GenStats)]),
+    "frn_generate_sampled": (_I, [_P, _P, _U32, _U32, ctypes.c_float, _U32, ctypes.c_float, ctypes.c_float,
+                                  ctypes.c_uint64, _P, _U32, _P, ctypes.POINTER(GenStats),
+                                  ctypes.POINTER(ctypes.c_uint64)]),
     "frn_synth_write": (_I, [ctypes.POINTER(SynthSpec), ctypes.c_char_p]),
     "frn_quantize": (_I, [_U32, _P, _SZ, _P]),
     "frn_gaussian": (_I, [_U64, _F, _SZ, _P]),
@@ -337,6 +340,21 @@ class Model:
                                          _ptr(stop) if stop.size else None, stop.size, _ptr(out),
                                          ctypes.byref(st)))
         return out[:st.n_generated].tolist(), st
+
+    def generate_sampled(self, prompt, max_new, temperature=0.7, top_k=40, top_p=0.9, repeat_penalty=1.0, seed=7,
+                         stop_ids=None):
+        """generate (generate.rs:83-157) with the device sampler; returns
+        (ids, stats, draws)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        stop = np.ascontiguousarray(self.stop_ids() if stop_ids is None else stop_ids, dtype=np.uint32)
+        out = np.zeros(max(max_new, 1), dtype=np.uint32)
+        st = GenStats()
+        draws = ctypes.c_uint64()
+        check(load().frn_generate_sampled(self.ctx, _ptr(prompt), prompt.size, max_new, float(temperature),
+                                          int(top_k), float(top_p), float(repeat_penalty), int(seed),
+                                          _ptr(stop) if stop.size else None, stop.size, _ptr(out),
+                                          ctypes.byref(st), ctypes.byref(draws)))
+        return out[:st.n_generated].tolist(), st, draws.value
 
     def timings_enable(self, on=True):
         check(load().frn_timings_enable(self.ctx, 1 if on else 0))

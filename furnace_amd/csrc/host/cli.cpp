@@ -38,12 +38,19 @@ static std::vector<uint32_t> parse_ids(const char* s) {
 }
 
 static int cmd_run(int argc, char** argv) {
-  if (argc < 1) return fprintf(stderr, "usage: furnace-hip run MODEL --prompt-ids a,b,c [-n N] [--max-ctx C] [--device D] [--timings]\n"), 2;
+  if (argc < 1)
+    return fprintf(stderr, "usage: furnace-hip run MODEL --prompt-ids a,b,c [-n N] [--temp T] [--top-k K] [--top-p P] "
+                           "[--repeat-penalty R] [--seed S] [--max-ctx C] [--device D] [--timings]\n"),
+           2;
   const char* model = argv[0];
   std::vector<uint32_t> ids;
   uint32_t max_new = 50, max_ctx = 0;
   int device = 0;
-  bool timings = false, eager = false;
+  bool timings = false, eager = false, have_seed = false;
+  // sampler settings and defaults of main.rs:42-58
+  float temp = 0.7f, top_p = 0.9f, repeat_penalty = 1.0f;
+  uint32_t top_k = 40;
+  uint64_t seed = 0;
   for (int i = 1; i < argc; ++i) {
     if (!strcmp(argv[i], "--prompt-ids") && i + 1 < argc) ids = parse_ids(argv[++i]);
     else if ((!strcmp(argv[i], "-n") || !strcmp(argv[i], "--max-tokens")) && i + 1 < argc) max_new = (uint32_t)atoi(argv[++i]);
@@ -51,8 +58,13 @@ static int cmd_run(int argc, char** argv) {
     else if (!strcmp(argv[i], "--device") && i + 1 < argc) device = atoi(argv[++i]);
     else if (!strcmp(argv[i], "--timings")) timings = true;
     else if (!strcmp(argv[i], "--eager")) eager = true;
-    else if (!strcmp(argv[i], "--temp") && i + 1 < argc) {
-      if (atof(argv[++i]) != 0.0) return fprintf(stderr, "Error: only --temp 0 (greedy) runs on the GPU path\n"), 2;
+    else if (!strcmp(argv[i], "--temp") && i + 1 < argc) temp = (float)atof(argv[++i]);
+    else if (!strcmp(argv[i], "--top-k") && i + 1 < argc) top_k = (uint32_t)atoi(argv[++i]);
+    else if (!strcmp(argv[i], "--top-p") && i + 1 < argc) top_p = (float)atof(argv[++i]);
+    else if (!strcmp(argv[i], "--repeat-penalty") && i + 1 < argc) repeat_penalty = (float)atof(argv[++i]);
+    else if (!strcmp(argv[i], "--seed") && i + 1 < argc) {
+      seed = strtoull(argv[++i], nullptr, 10);
+      have_seed = true;
     } else return fprintf(stderr, "Error: unknown argument %s\n", argv[i]), 2;
   }
   if (ids.empty()) return fprintf(stderr, "Error: --prompt-ids is required\n"), 2;
@@ -82,13 +94,24 @@ static int cmd_run(int argc, char** argv) {
   frn_timings_enable(ctx, timings);
   std::vector<uint32_t> out(max_new);
   frn_gen_stats st;
-  if (frn_generate_greedy(ctx, ids.data(), (uint32_t)ids.size(), max_new, stop, n_stop, out.data(), &st)) return die("generate");
+  uint64_t draws = 0;
+  if (temp == 0.0f) {
+    if (frn_generate_greedy(ctx, ids.data(), (uint32_t)ids.size(), max_new, stop, n_stop, out.data(), &st))
+      return die("generate");
+  } else {
+    if (!have_seed) seed = (uint64_t)time(nullptr);  // main.rs:253-259: one drawn from the clock
+    fprintf(stderr, "sampler: temp %g top-k %u top-p %g repeat-penalty %g seed %llu\n", (double)temp, top_k,
+            (double)top_p, (double)repeat_penalty, (unsigned long long)seed);
+    if (frn_generate_sampled(ctx, ids.data(), (uint32_t)ids.size(), max_new, temp, top_k, top_p, repeat_penalty,
+                             seed, stop, n_stop, out.data(), &st, &draws))
+      return die("generate");
+  }
   fprintf(stderr, "prefill: %zu tokens in %.2f s (%.2f ms/token)\n", ids.size(), st.prefill_s,
           st.prefill_s * 1000.0 / ids.size());
   if (st.decode_steps)
     fprintf(stderr, "decode: %u steps, %.3f ms/token average (%.1f tokens/s)\n", st.decode_steps,
             st.decode_s * 1000.0 / st.decode_steps, st.decode_steps / st.decode_s);
-  fprintf(stderr, "sampler: 0 RNG draws\n");
+  fprintf(stderr, "sampler: %llu RNG draws\n", (unsigned long long)draws);
   fprintf(stderr, "generated ids: [");
   for (uint32_t i = 0; i < st.n_generated; ++i) fprintf(stderr, "%s%u", i ? ", " : "", out[i]);
   fprintf(stderr, "]\n");

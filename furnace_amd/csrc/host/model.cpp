@@ -7,6 +7,7 @@
 #include <time.h>
 
 #include <string>
+#include <vector>
 
 #include "../../../include/furnace_host.h"
 #include "../common.hpp"
@@ -150,5 +151,38 @@ extern "C" frn_status frn_generate_greedy(frn_ctx* ctx, const uint32_t* prompt, 
     s.decode_steps += 1;
   }
   if (stats) *stats = s;
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_generate_sampled(frn_ctx* ctx, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                                           float temperature, uint32_t top_k, float top_p, float repeat_penalty,
+                                           uint64_t seed, const uint32_t* stop_ids, uint32_t n_stop, uint32_t* out_ids,
+                                           frn_gen_stats* stats, uint64_t* draws) {
+  if (!ctx || !prompt || !out_ids) return frn_fail(FRN_EINVAL, "frn_generate_sampled: null argument");
+  frn_status st = frn_sampler_init(ctx, temperature, top_k, top_p, repeat_penalty, seed);
+  if (st) return st;
+  frn_gen_stats s{};
+  const uint32_t window = 64;  // Sampler::repeat_window (sampler.rs:75)
+  std::vector<uint32_t> context(prompt, prompt + n_prompt);
+  uint32_t next = 0;
+  double t0 = now_s();
+  if ((st = frn_prefill(ctx, prompt, n_prompt, &next))) return st;
+  s.prefill_s = now_s() - t0;
+  for (uint32_t step = 0; step < max_new; ++step) {
+    const size_t w = context.size() > window ? context.size() - window : 0;  // generate.rs:123
+    if ((st = frn_sample(ctx, context.data() + w, (uint32_t)(context.size() - w), &next))) return st;
+    bool stop = false;
+    for (uint32_t i = 0; i < n_stop; ++i) stop |= stop_ids[i] == next;
+    if (stop) break;
+    out_ids[s.n_generated++] = next;
+    context.push_back(next);
+    if (step + 1 == max_new) break;
+    double t1 = now_s();
+    if ((st = frn_decode(ctx, next, nullptr))) return st;
+    s.decode_s += now_s() - t1;
+    s.decode_steps += 1;
+  }
+  if (stats) *stats = s;
+  if (draws && (st = frn_sampler_draws(ctx, draws))) return st;
   return FRN_OK;
 }

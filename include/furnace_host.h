@@ -49,6 +49,15 @@ typedef struct frn_gen_stats {
 frn_status frn_generate_greedy(frn_ctx* ctx, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
                                const uint32_t* stop_ids, uint32_t n_stop, uint32_t* out_ids, frn_gen_stats* stats);
 
+/* generate (generate.rs:83-157) with the device sampler: prefill, then
+ * sample with Sampler::new(temperature, top_k, top_p, repeat_penalty, seed)
+ * over the last 64 context ids (generate.rs:123) / stop check / decode, as
+ * frn_generate_greedy.  *draws receives Sampler::draws (may be NULL). */
+frn_status frn_generate_sampled(frn_ctx* ctx, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                                float temperature, uint32_t top_k, float top_p, float repeat_penalty, uint64_t seed,
+                                const uint32_t* stop_ids, uint32_t n_stop, uint32_t* out_ids, frn_gen_stats* stats,
+                                uint64_t* draws);
+
 /* ---- synthetic models ------------------------------------------------------ */
 enum { FRN_MIX_ALL_Q8_0 = 0, FRN_MIX_Q4_K_M = 1, FRN_MIX_ALL_Q4_K = 2, FRN_MIX_ALL_Q6_K = 3, FRN_MIX_ALL_Q5_0 = 4,
        FRN_MIX_ALL_F32 = 5 };
