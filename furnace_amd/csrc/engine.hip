@@ -97,8 +97,11 @@ struct frn_ctx {
   uint32_t len = 0;           // host view of KvCache::len
   uint32_t last_next = 0xFFFFFFFFu;
   bool finalized = false, have_logits = false;
-  hipGraphExec_t g_step = nullptr, g_prefill = nullptr;
-  hipGraph_t graph_step = nullptr, graph_prefill = nullptr;
+  // captured steps: [0] short contexts, [1] past ATTENTION_LONG_FROM positions
+  hipGraphExec_t g_step[2] = {}, g_prefill[2] = {};
+  hipGraph_t graph_step[2] = {}, graph_prefill[2] = {};
+  bool rec_long = false;  // the form record_step records (long-context attention)
+  float* att = nullptr;   // [n_heads * head_dim] merged attention output (long-context form)
   // --timings: the step runs eagerly with an event pair around each kernel
   bool timing = false;
   std::vector<hipEvent_t> ev;
@@ -109,13 +112,15 @@ struct frn_ctx {
 
 static void free_ctx(frn_ctx* c) {
   if (!c) return;
-  if (c->g_step) (void)hipGraphExecDestroy(c->g_step);
-  if (c->g_prefill) (void)hipGraphExecDestroy(c->g_prefill);
-  if (c->graph_step) (void)hipGraphDestroy(c->graph_step);
-  if (c->graph_prefill) (void)hipGraphDestroy(c->graph_prefill);
+  for (int i = 0; i < 2; ++i) {
+    if (c->g_step[i]) (void)hipGraphExecDestroy(c->g_step[i]);
+    if (c->g_prefill[i]) (void)hipGraphExecDestroy(c->g_prefill[i]);
+    if (c->graph_step[i]) (void)hipGraphDestroy(c->graph_step[i]);
+    if (c->graph_prefill[i]) (void)hipGraphDestroy(c->graph_prefill[i]);
+  }
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part, c->hist, c->rng, c->cand_v, c->cand_id, c->recent, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -192,7 +197,7 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
       (e = alloc_prefill(x)) ||
       (e = dmalloc(&x->hist, (size_t)c.max_ctx * 4)) ||
       (e = hipHostMalloc((void**)&x->h_hist, GREEDY_BATCH * 4, hipHostMallocDefault)) ||
-      (e = dmalloc(&x->rng, sizeof(SamplerRng))) ||
+      (e = dmalloc(&x->rng, sizeof(SamplerRng))) || (e = dmalloc(&x->att, qd * 4)) ||
       (e = dmalloc(&x->cand_v, (size_t)sampler_blocks(c.vocab) * SAMPLER_MAX_K * 4)) ||
       (e = dmalloc(&x->cand_id, (size_t)sampler_blocks(c.vocab) * SAMPLER_MAX_K * 4)) ||
       (e = dmalloc(&x->recent, SAMPLER_MAX_RECENT * 4)) ||
@@ -301,11 +306,15 @@ struct Tick {
   bool on;
   size_t n = 0;
   int rcat = -1, rlayer = -1, layer = -1;  // rlayer -1: every layer
-  uint32_t reps = 0, launched = 0;
+  int counted = -2;                        // the last layer counted in `launched`
+  uint32_t reps = 0, launched = 0;         // category instances replayed (one per layer)
   template <class F>
   hipError_t replay(int cat, F&& launch) {
     if (cat != rcat || (layer >= 0 && rlayer >= 0 && layer != rlayer)) return hipSuccess;
-    ++launched;
+    if (layer != counted || layer < 0) {  // a category of two launches in a layer counts once
+      launched += reps;
+      counted = layer;
+    }
     for (uint32_t r = 0; r < reps; ++r)
       if (hipError_t e = launch()) return e;
     return hipSuccess;
@@ -336,6 +345,7 @@ struct Tick {
 // replayed graphs, or eagerly with per-kernel events when tk.on.
 static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
   const frn_config& g = c->cfg;
+  tk.counted = -2;
   hipStream_t s = c->stream;
   hipError_t e;
   float scale = 1.0f / sqrtf((float)g.head_dim);  // model.rs:384
@@ -378,18 +388,28 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
     if (TIMED(CAT_QKV, launch_gemv(qkv, GEMV_STORE, s))) return e;
     // rope, KV append, attention (model.rs:460-467)
     size_t lo = (size_t)l * g.max_ctx * g.n_kv_heads * g.head_dim;
+    const uint32_t cap = c->rec_long ? ATTENTION_MAX_SPLITS_LONG : ATTENTION_MAX_SPLITS;
     if (TIMED(CAT_ATTN, launch_attention(c->q, c->k, c->v, c->rope, c->kcache + lo, c->vcache + lo, g.n_heads,
-                                         g.n_kv_heads, g.head_dim, g.max_ctx, scale, c->part, c->st, s)))
+                                         g.n_kv_heads, g.head_dim, g.max_ctx, scale, c->part, c->st, cap, s)))
       return e;
-    // merge of the attention splits + o-proj + residual (model.rs:436-438, 469-470)
-    GemvArgs o = args(QD, nullptr, nullptr);
-    o.seg[0] = seg(L.wo, nullptr, nullptr, c->x, c->x);
-    o.att_part = c->part;
-    o.st = c->st;
-    o.att_ms = attention_splits(g.max_ctx);
-    o.att_hd = g.head_dim;
-    o.att_part_bytes = (uint32_t)(attention_part_floats(g.n_heads, g.head_dim, g.max_ctx) * 4);
-    if (TIMED(CAT_OPROJ, launch_gemv(o, GEMV_RESID_ATT, s))) return e;
+    if (c->rec_long) {
+      // long contexts: up to 64 splits, merged once (model.rs:436-438),
+      // then o-proj + residual on the merged rows (model.rs:469-470)
+      if (TIMED(CAT_ATTN, launch_attn_merge(c->part, c->att, g.n_heads, g.head_dim, g.max_ctx, c->st, s))) return e;
+      GemvArgs o = args(QD, c->att, nullptr);
+      o.seg[0] = seg(L.wo, nullptr, nullptr, c->x, c->x);
+      if (TIMED(CAT_OPROJ, launch_gemv(o, GEMV_RESID, s))) return e;
+    } else {
+      // merge of the attention splits + o-proj + residual (model.rs:436-438, 469-470)
+      GemvArgs o = args(QD, nullptr, nullptr);
+      o.seg[0] = seg(L.wo, nullptr, nullptr, c->x, c->x);
+      o.att_part = c->part;
+      o.st = c->st;
+      o.att_ms = attention_splits(g.max_ctx);
+      o.att_hd = g.head_dim;
+      o.att_part_bytes = (uint32_t)(attention_part_floats(g.n_heads, g.head_dim, g.max_ctx) * 4);
+      if (TIMED(CAT_OPROJ, launch_gemv(o, GEMV_RESID_ATT, s))) return e;
+    }
     // rmsnorm + gate/up + SwiGLU (model.rs:473-476)
     GemvArgs gu = args(H, c->x, L.ffn_norm);
     gu.seg[0] = seg(L.gate, L.up, nullptr, c->act, nullptr);
@@ -486,8 +506,12 @@ extern "C" frn_status frn_finalize(frn_ctx* c) {
   }
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
   if (!(g.flags & FRN_FLAG_EAGER)) {
-    if ((st = capture(c, true, &c->graph_step, &c->g_step))) return st;
-    if ((st = capture(c, false, &c->graph_prefill, &c->g_prefill))) return st;
+    for (int lng = 0; lng < (g.max_ctx > ATTENTION_LONG_FROM ? 2 : 1); ++lng) {
+      c->rec_long = lng;
+      if ((st = capture(c, true, &c->graph_step[lng], &c->g_step[lng]))) return st;
+      if ((st = capture(c, false, &c->graph_prefill[lng], &c->g_prefill[lng]))) return st;
+    }
+    c->rec_long = false;
   }
   c->finalized = true;
   return FRN_OK;
@@ -502,13 +526,16 @@ static frn_status run_step(frn_ctx* c, uint32_t tok, bool with_logits, bool on_d
     HIP_TRY(hipMemcpyAsync((char*)c->st + offsetof(StepState, tok), &c->h_st->tok, 4, hipMemcpyHostToDevice, c->stream),
             "token upload");
   }
+  // the long-context form once the step covers more than ATTENTION_LONG_FROM positions
+  c->rec_long = c->len + 1 > ATTENTION_LONG_FROM;
   if (c->timing) {
     HIP_TRY(timed_step(c, with_logits), "timed step");
   } else if (c->cfg.flags & FRN_FLAG_EAGER) {
     Tick tk{c, false};
     HIP_TRY(record_step(c, with_logits, tk), "eager step");
   } else {
-    HIP_TRY(hipGraphLaunch(with_logits ? c->g_step : c->g_prefill, c->stream), "hipGraphLaunch");
+    HIP_TRY(hipGraphLaunch(with_logits ? c->g_step[c->rec_long] : c->g_prefill[c->rec_long], c->stream),
+            "hipGraphLaunch");
   }
   c->len += 1;
   c->last_next = 0xFFFFFFFFu;
@@ -855,6 +882,7 @@ extern "C" frn_status frn_bench_kernel(frn_ctx* c, const char* name, uint32_t la
     (void)hipEventDestroy(e0);
     return fail(FRN_EHIP, "hipEventCreate: %s", hipGetErrorString(r));
   }
+  c->rec_long = c->len + 1 > ATTENTION_LONG_FROM;  // the form the next step runs
   Tick tk{c, false};
   tk.rcat = cat;
   tk.rlayer = layer == FRN_ALL_LAYERS ? -1 : (int)layer;

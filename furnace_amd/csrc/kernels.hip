@@ -8,9 +8,9 @@
 namespace frn {
 
 constexpr int ATT_CHUNK = ATTENTION_CHUNK;  // positions per attention block (one wave per softmax row)
-uint32_t attention_splits(uint32_t max_ctx) {
+uint32_t attention_splits(uint32_t max_ctx, uint32_t cap) {
   const uint32_t t = (max_ctx + ATT_CHUNK - 1) / ATT_CHUNK;
-  return t < ATTENTION_MAX_SPLITS ? t : ATTENTION_MAX_SPLITS;
+  return t < cap ? t : cap;
 }
 
 // ---- reductions -----------------------------------------------------------
@@ -772,7 +772,7 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
                                                    const float* __restrict__ vn, const float* __restrict__ cs,
                                                    float* __restrict__ kc, float* __restrict__ vc, uint32_t nh,
                                                    uint32_t nkv, uint32_t max_splits, uint32_t max_ctx, float scale,
-                                                   float* __restrict__ part, const StepState* st) {
+                                                   float* __restrict__ part, const StepState* st, uint32_t cap) {
   constexpr int C = ATT_CHUNK, TPP = 256 / C, DPT = HD / TPP, PARTS = 256 / HD, HALF = HD / 2, NP = C / PARTS;
   constexpr int RR = (GQ * HALF + HALF + 255) / 256;  // rotation rounds per thread
   // global loads: thread t moves float4 column lc of rows lr + RPI*i, so a
@@ -817,7 +817,7 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
   }
   const float vnew = vn[(size_t)g * HD + (threadIdx.x % HD)];
   const uint32_t pos = st->pos, T = pos + 1;
-  const uint32_t len = attention_split_len(T), t0 = split * len;
+  const uint32_t len = attention_split_len(T, cap), t0 = split * len;
   if (t0 >= T) return;
   const uint32_t ns = (T + len - 1) / len, tend = min(t0 + len, T), nsub = (tend - t0 + C - 1) / C;
   // rows of sub-tile k this thread loads: cached positions < pos only; the
@@ -953,24 +953,64 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
 }
 
 size_t attention_part_floats(uint32_t nh, uint32_t hd, uint32_t max_ctx) {
-  return (size_t)nh * attention_splits(max_ctx) * (hd + 2);
+  return (size_t)nh * attention_splits(max_ctx, ATTENTION_MAX_SPLITS_LONG) * (hd + 2);
+}
+
+// Long-context merge of the splits of one query head (block h, thread d):
+// the split maxima and sums go through LDS, then each thread combines its
+// dimension over the splits (their loads independent of each other).
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_merge(const float* __restrict__ part, float* __restrict__ out,
+                                                   uint32_t ms, const StepState* st) {
+  __shared__ float msl[2 * ATTENTION_MAX_SPLITS_LONG];
+  const uint32_t h = blockIdx.x, d = threadIdx.x;
+  const uint32_t T = st->pos + 1, len = attention_split_len(T, ATTENTION_MAX_SPLITS_LONG);
+  const uint32_t ns = (T + len - 1) / len;
+  const float* base = part + (size_t)h * ms * (HD + 2);
+  for (uint32_t sp = d; sp < ns; sp += HD) {
+    msl[2 * sp] = base[(size_t)sp * (HD + 2) + HD];
+    msl[2 * sp + 1] = base[(size_t)sp * (HD + 2) + HD + 1];
+  }
+  __syncthreads();
+  float M = -INFINITY;
+  for (uint32_t sp = 0; sp < ns; ++sp) M = fmaxf(M, msl[2 * sp]);
+  float o = 0.f, L = 0.f;
+#pragma unroll 8
+  for (uint32_t sp = 0; sp < ns; ++sp) {
+    const float e = expf(msl[2 * sp] - M);  // model.rs:371-438, evaluated split-wise
+    L += e * msl[2 * sp + 1];
+    o += e * base[(size_t)sp * (HD + 2) + d];
+  }
+  out[(size_t)h * HD + d] = L > 0.f ? o / L : 0.f;
+}
+
+hipError_t launch_attn_merge(const float* part, float* out, uint32_t nh, uint32_t hd, uint32_t max_ctx,
+                             const StepState* st, hipStream_t s) {
+  const uint32_t ms = attention_splits(max_ctx, ATTENTION_MAX_SPLITS_LONG);
+  if (hd == 128)
+    hipLaunchKernelGGL(k_attn_merge<128>, dim3(nh), dim3(128), 0, s, part, out, ms, st);
+  else if (hd == 64)
+    hipLaunchKernelGGL(k_attn_merge<64>, dim3(nh), dim3(64), 0, s, part, out, ms, st);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 template <int HD, int GQ>
 static void att_go(dim3 grid, hipStream_t s, const float* q, const float* k, const float* v, const float* cs,
                    float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms, uint32_t max_ctx, float scale,
-                   float* part, const StepState* st) {
+                   float* part, const StepState* st, uint32_t cap) {
   hipLaunchKernelGGL((k_attention<HD, GQ>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale,
-                     part, st);
+                     part, st, cap);
 }
 
 template <int HD>
 static hipError_t att_gq(uint32_t gq, dim3 grid, hipStream_t s, const float* q, const float* k, const float* v,
                          const float* cs, float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms,
-                         uint32_t max_ctx, float scale, float* part, const StepState* st) {
+                         uint32_t max_ctx, float scale, float* part, const StepState* st, uint32_t cap) {
   switch (gq) {
 #define FRN_ATT_GQ(n) \
-  case n: att_go<HD, n>(grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st); break;
+  case n: att_go<HD, n>(grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st, cap); break;
     FRN_ATT_GQ(1) FRN_ATT_GQ(2) FRN_ATT_GQ(3) FRN_ATT_GQ(4) FRN_ATT_GQ(5) FRN_ATT_GQ(6) FRN_ATT_GQ(7) FRN_ATT_GQ(8)
 #undef FRN_ATT_GQ
     default: return hipErrorInvalidValue;
@@ -985,12 +1025,13 @@ bool attention_supported(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_di
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, const float* cs, float* kc, float* vc,
                             uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx, float scale, float* part,
-                            const StepState* st, hipStream_t s) {
-  if (!attention_supported(nh, nkv, hd)) return hipErrorInvalidValue;
-  uint32_t ms = attention_splits(max_ctx), gq = nh / nkv;
+                            const StepState* st, uint32_t cap, hipStream_t s) {
+  if (!attention_supported(nh, nkv, hd) || (cap != ATTENTION_MAX_SPLITS && cap != ATTENTION_MAX_SPLITS_LONG))
+    return hipErrorInvalidValue;
+  uint32_t ms = attention_splits(max_ctx, cap), gq = nh / nkv;
   dim3 grid(nkv, ms);
-  if (hd == 128) return att_gq<128>(gq, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st);
-  return att_gq<64>(gq, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st);
+  if (hd == 128) return att_gq<128>(gq, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st, cap);
+  return att_gq<64>(gq, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st, cap);
 }
 
 // ---- step bookkeeping and argmax (generate.rs:69-77) ------------------------

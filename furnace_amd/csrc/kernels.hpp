@@ -59,22 +59,35 @@ uint32_t gemv_blocks(uint32_t type, uint32_t rows, uint32_t in);
 
 hipError_t launch_embed(const uint8_t* table, uint32_t type, uint32_t hidden, uint32_t row_bytes, StepState* st,
                         float* x, hipStream_t s);
+constexpr uint32_t ATTENTION_CHUNK = 64;  // positions per attention sub-tile
+// At most 16 splits while the o-proj GEMV merges them in its staging
+// (GEMV_RESID_ATT: one or two batches of loads); at most 64 in the
+// long-context step, whose splits k_attn_merge merges once.
+constexpr uint32_t ATTENTION_MAX_SPLITS = 16;
+constexpr uint32_t ATTENTION_MAX_SPLITS_LONG = 64;
+// Steps over more positions than this (pos + 1) run the long-context form.
+constexpr uint32_t ATTENTION_LONG_FROM = 1024;
 // RoPE(q), RoPE(k) at the step's position, KV-cache append and
-// split-sequence GQA attention in one launch; writes the per-split partials
-// that a GEMV_RESID_ATT launch merges (layout in GemvArgs).
+// split-sequence GQA attention in one launch, with at most `cap` splits;
+// writes the per-split partials that a GEMV_RESID_ATT launch (cap 16) or
+// launch_attn_merge (cap 64) merges (layout in GemvArgs).
 hipError_t launch_attention(const float* q, const float* k, const float* v, const float* rope_cs, float* k_cache,
                             float* v_cache, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                            uint32_t max_ctx, float scale, float* part, const StepState* st, hipStream_t s);
+                            uint32_t max_ctx, float scale, float* part, const StepState* st, uint32_t cap,
+                            hipStream_t s);
+// The long-context merge: out[h][d] = sum_s e^(m_s - M) o_s[d] / sum_s
+// e^(m_s - M) l_s over the step's splits, one block per query head.
+hipError_t launch_attn_merge(const float* part, float* out, uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx,
+                             const StepState* st, hipStream_t s);
+// partials buffer: n_heads x attention_splits(max_ctx, 64) x (head_dim + 2)
 size_t attention_part_floats(uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx);
-uint32_t attention_splits(uint32_t max_ctx);  // att_ms: the most splits a step can have
-constexpr uint32_t ATTENTION_CHUNK = 64;      // positions per attention sub-tile
-constexpr uint32_t ATTENTION_MAX_SPLITS = 16;
+// the most splits a step can have with at most `cap` (att_ms for cap 16)
+uint32_t attention_splits(uint32_t max_ctx, uint32_t cap = ATTENTION_MAX_SPLITS);
 // Positions per split for a step over T positions: whole 64-position
-// sub-tiles, as few as keep the step at <= 16 splits (the merge of the
-// splits then stays one or two batches of loads).
-__host__ __device__ inline uint32_t attention_split_len(uint32_t T) {
+// sub-tiles, as few as keep the step at <= cap splits.
+__host__ __device__ inline uint32_t attention_split_len(uint32_t T, uint32_t cap = ATTENTION_MAX_SPLITS) {
   const uint32_t tiles = (T + ATTENTION_CHUNK - 1) / ATTENTION_CHUNK;
-  return ATTENTION_CHUNK * ((tiles + ATTENTION_MAX_SPLITS - 1) / ATTENTION_MAX_SPLITS);
+  return ATTENTION_CHUNK * ((tiles + cap - 1) / cap);
 }
 // Shapes the attention kernel handles: head_dim 64 or 128, at most 8 query
 // heads per kv head.
