@@ -172,21 +172,31 @@ struct XStage {
   float2 pm[ATT ? NX : 1][NB];
   float4 po[ATT ? NX : 1][NB][2];
   uint32_t ns = 0;
-  __device__ __forceinline__ uint32_t part_off(const GemvArgs& a, uint32_t u, uint32_t sp) const {
-    const uint32_t h = 8u * u / a.att_hd, d0 = 8u * u % a.att_hd;
-    return 4u * ((h * a.att_ms + sp) * (a.att_hd + 2) + d0);
-  }
-  __device__ __forceinline__ void load_batch(const GemvArgs& a, rsrc_t rp, uint32_t sp0) {
+  // per group i: byte offset of split 0 of its 8 values (BUF_INVALID: no
+  // group) and from there to the split's (m, l); bytes per split.  The
+  // divisions by the head size happen once here, so the per-split offsets
+  // are selects (a division in the offset made the compiler branch around
+  // every load and re-read the kernel arguments each time).
+  uint32_t pbase[ATT ? NX : 1], pml[ATT ? NX : 1], pstride = 0;
+  __device__ __forceinline__ void att_setup(const GemvArgs& a) {
+    pstride = 4u * (a.att_hd + 2);
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      const uint32_t u = threadIdx.x + 256u * i;
+      const uint32_t u = threadIdx.x + 256u * i, h = 8u * u / a.att_hd, d0 = 8u * u % a.att_hd;
+      pbase[i] = u < a.in / 8 ? 4u * (h * a.att_ms * (a.att_hd + 2) + d0) : BUF_INVALID;
+      pml[i] = 4u * (a.att_hd - d0);
+    }
+  }
+  __device__ __forceinline__ void load_batch(rsrc_t rp, uint32_t sp0) {
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const uint32_t sp = sp0 + b;
-        const uint32_t o = (u < a.in / 8 && sp < ns) ? part_off(a, u, sp) : BUF_INVALID;
+        const uint32_t o = (pbase[i] != BUF_INVALID && sp < ns) ? pbase[i] + sp * pstride : BUF_INVALID;
         po[i][b][0] = u4f(bl128(rp, o));
         po[i][b][1] = u4f(bl128(rp, o + 16u));
-        const uint2 q = bl64(rp, o == BUF_INVALID ? BUF_INVALID : o - 4u * (8u * u % a.att_hd) + 4u * a.att_hd);
+        const uint2 q = bl64(rp, o == BUF_INVALID ? BUF_INVALID : o + pml[i]);
         pm[i][b] = make_float2(__uint_as_float(q.x), __uint_as_float(q.y));
       }
     }
@@ -196,7 +206,8 @@ struct XStage {
   // overlap the read of st->pos
   __device__ __forceinline__ void load_att(const GemvArgs& a, rsrc_t rp) {
     ns = NB;
-    load_batch(a, rp, 0);
+    att_setup(a);
+    load_batch(rp, 0);
     const uint32_t T = a.st->pos + 1, len = attention_split_len(T);
     ns = (T + len - 1) / len;
   }
@@ -213,7 +224,7 @@ struct XStage {
       for (int k = 0; k < 8; ++k) o[i][k] = 0.f;
     }
     for (uint32_t sp0 = 0; sp0 < ns; sp0 += NB) {
-      if (sp0) load_batch(a, rp, sp0);
+      if (sp0) load_batch(rp, sp0);
 #pragma unroll
       for (int i = 0; i < NX; ++i) {
         float Mb = M[i];
