@@ -15,13 +15,13 @@ LIB_PATH = os.path.join(_PKG, "lib", "libfurnace_hip.so")
 CLI_PATH = os.path.join(_PKG, "bin", "furnace-hip")
 
 # ggml type codes (src/gguf.rs:180-201)
-F32, Q5_0, Q8_0, Q4_K, Q6_K = 0, 6, 8, 12, 14
-BLOCK = {F32: (1, 4), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+F32, F16, Q5_0, Q8_0, Q4_K, Q6_K = 0, 1, 6, 8, 12, 14
+BLOCK = {F32: (1, 4), F16: (1, 2), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 
 FLAG_EAGER = 1  # FRN_FLAG_EAGER
 FLAG_STEPWISE_PREFILL = 2  # FRN_FLAG_STEPWISE_PREFILL
 
-MIX_ALL_Q8_0, MIX_Q4_K_M, MIX_ALL_Q4_K, MIX_ALL_Q6_K, MIX_ALL_Q5_0, MIX_ALL_F32 = range(6)
+MIX_ALL_Q8_0, MIX_Q4_K_M, MIX_ALL_Q4_K, MIX_ALL_Q6_K, MIX_ALL_Q5_0, MIX_ALL_F32, MIX_Q4_K_M_LLAMA, MIX_ALL_F16 = range(8)
 
 STATUS = {0: "FRN_OK", 1: "FRN_EINVAL", 2: "FRN_EDTYPE", 3: "FRN_ESHAPE", 4: "FRN_ECTX_OVERFLOW",
           5: "FRN_ETOKEN", 6: "FRN_EOOM", 7: "FRN_EHIP", 8: "FRN_ENODEV"}

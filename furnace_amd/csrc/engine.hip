@@ -52,7 +52,11 @@ struct LayerPtrs {
 };
 
 size_t type_row_bytes(uint32_t t, uint64_t in) { return (size_t)(in / blk_elems(t)) * blk_bytes(t); }
-bool known_type(uint32_t t) { return t == T_F32 || t == T_Q5_0 || t == T_Q8_0 || t == T_Q4_K || t == T_Q6_K; }
+// F16 is an extension: the reference's dequantize has no F16 arm and its
+// Model::load rejects such tensors (src/quant.rs:279)
+bool known_type(uint32_t t) {
+  return t == T_F32 || t == T_F16 || t == T_Q5_0 || t == T_Q8_0 || t == T_Q4_K || t == T_Q6_K;
+}
 
 // Kernel categories of the --timings dashboard.  furnace's perf.rs counters
 // (matmul, rmsnorm, rope, attn, add/swiglu, embed, sample) map onto these

@@ -23,7 +23,7 @@
 
 namespace frn {
 
-enum : uint32_t { T_F32 = 0, T_Q5_0 = 6, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum : uint32_t { T_F32 = 0, T_F16 = 1, T_Q5_0 = 6, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
 
 // ---- cross-lane all-reduce ----------------------------------------------------
 // All-reduce over aligned groups of W lanes (W a power of two up to 64):
@@ -66,10 +66,10 @@ __device__ __forceinline__ T group_reduce(T v, Op op = Op()) {
 }
 
 __host__ __device__ constexpr int blk_elems(uint32_t t) {
-  return t == T_Q4_K || t == T_Q6_K ? 256 : (t == T_F32 ? 1 : 32);
+  return t == T_Q4_K || t == T_Q6_K ? 256 : (t == T_F32 || t == T_F16 ? 1 : 32);
 }
 __host__ __device__ constexpr int blk_bytes(uint32_t t) {
-  return t == T_Q4_K ? 144 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 34 : t == T_Q5_0 ? 22 : 4;
+  return t == T_Q4_K ? 144 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 34 : t == T_Q5_0 ? 22 : t == T_F16 ? 2 : 4;
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
@@ -108,7 +108,9 @@ __device__ __forceinline__ void q4k_scale_min_regs(uint32_t a, uint32_t b, uint3
 
 // Value i of one block (quant.rs:17-42, 53-63, 93-109, 114-133).
 __device__ __forceinline__ float decode_elem(uint32_t t, const uint8_t* b, int i) {
-  if (t == T_Q8_0) {
+  if (t == T_F16) {  // IEEE half -> single, exact (a format the reference does not load)
+    return f16_bits_to_f32(ld_u16(b));
+  } else if (t == T_Q8_0) {
     return f16_bits_to_f32(ld_u16(b)) * (float)(int8_t)b[2 + i];
   } else if (t == T_Q5_0) {
     float d = f16_bits_to_f32(ld_u16(b));

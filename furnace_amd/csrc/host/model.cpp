@@ -105,7 +105,9 @@ extern "C" frn_status frn_model_load(const frn_gguf* g, int device, uint32_t max
     const uint8_t* p;
     size_t bytes;
     if ((st = frn_host::tensor(g->f, t.name, &info, &p, &bytes))) break;
-    if (t.type != 0 && t.type != 6 && t.type != 8 && t.type != 12 && t.type != 14) {
+    // F16 (type 1) is an extension: the reference's Model::load rejects it
+    // (src/quant.rs:279)
+    if (t.type != 0 && t.type != 1 && t.type != 6 && t.type != 8 && t.type != 12 && t.type != 14) {
       st = frn_fail(FRN_EDTYPE, "tensor '%s': dequantization for ggml type %u is not implemented", t.name.c_str(), t.type);
       break;
     }

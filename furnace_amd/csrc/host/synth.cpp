@@ -188,8 +188,11 @@ void enc_q6_k(const float* x, uint8_t* b) {  // 210 B
   }
 }
 
+void enc_f16(const float* x, uint8_t* b) { put16(b, f32_to_f16(x[0])); }  // IEEE half, round to nearest even
+
 bool encoder(uint32_t type, void (**f)(const float*, uint8_t*), int* be, int* bb) {
   switch (type) {
+    case 1: *f = enc_f16; *be = 1; *bb = 2; return true;
     case 8: *f = enc_q8_0; *be = 32; *bb = 34; return true;
     case 6: *f = enc_q5_0; *be = 32; *bb = 22; return true;
     case 12: *f = enc_q4_k; *be = 256; *bb = 144; return true;
@@ -240,6 +243,7 @@ struct TSpec {
 uint64_t tensor_bytes(uint32_t type, uint64_t n) {
   switch (type) {
     case 0: return n * 4;
+    case 1: return n * 2;
     case 8: return n / 32 * 34;
     case 6: return n / 32 * 22;
     case 12: return n / 256 * 144;
@@ -281,6 +285,15 @@ extern "C" frn_status frn_synth_write(const frn_synth_spec* sp, const char* path
       case FRN_MIX_ALL_Q6_K: return 14;
       case FRN_MIX_ALL_Q5_0: return 6;
       case FRN_MIX_ALL_F32: return 0;
+      case FRN_MIX_ALL_F16: return 1;
+      case FRN_MIX_Q4_K_M_LLAMA: {
+        // llama.cpp's Q4_K_M (llama_tensor_get_type, use_more_bits): Q6_K
+        // for attn_v and ffn_down on the first and last eighth of the
+        // layers and on every third layer between them, Q4_K elsewhere
+        const uint32_t n = S.n_layers, e = n / 8;
+        const bool more = layer < e || layer >= 7 * n / 8 || (layer - e) % 3 == 2;
+        return ((which == 2 || which == 6) && more) ? 14 : 12;
+      }
       default:  // Q4_K_M: Q6_K for attn_v and ffn_down on even layers
         return ((which == 2 || which == 6) && layer % 2 == 0) ? 14 : 12;
     }
@@ -310,7 +323,7 @@ extern "C" frn_status frn_synth_write(const frn_synth_spec* sp, const char* path
   add("output_norm.weight", H, 1, 0, 1);
   if (!S.tied) add("output.weight", H, S.vocab, S.output_type, 0);
   for (auto& t : ts) {
-    size_t be = t.type == 12 || t.type == 14 ? 256 : t.type == 0 ? 1 : 32;
+    size_t be = t.type == 12 || t.type == 14 ? 256 : t.type <= 1 ? 1 : 32;
     if (t.in % be) return frn_fail(FRN_ESHAPE, "tensor %s: in dim %llu not a multiple of %zu", t.name.c_str(),
                                    (unsigned long long)t.in, be);
   }

@@ -53,7 +53,7 @@ hipError_t launch_dequant(uint32_t type, const uint8_t* raw, size_t n, float* ou
 __host__ __device__ inline int items_per_row(uint32_t t, uint32_t in, bool pairs) {
   if (t == T_Q4_K || t == T_Q6_K) return (int)(in / 256) * 8;
   if (t == T_Q8_0 || t == T_Q5_0) return (int)(pairs ? in / 64 : in / 32);
-  return (int)(in / 16);  // F32: 16 floats per item
+  return (int)(in / 16);  // F32, F16: 16 values per item
 }
 
 // Items of one row a lane loads per pipeline step: 3 for the K-quants, 2
@@ -150,6 +150,36 @@ struct Fmt<T_F32> {  // 16 floats per item
       float4 b = Xp[i];
       s += __uint_as_float(w.w[i].x) * b.x + __uint_as_float(w.w[i].y) * b.y + __uint_as_float(w.w[i].z) * b.z +
            __uint_as_float(w.w[i].w) * b.w;
+    }
+    return s;
+  }
+};
+
+struct F16Raw {
+  uint4 w[2];
+};
+template <>
+struct Fmt<T_F16> {  // 16 halves per item (a format the reference does not load)
+  using Raw = F16Raw;
+  static constexpr int NC = 0;
+  static __device__ __forceinline__ uint32_t chunk(int, int, bool) { return 0u; }
+  static __device__ __forceinline__ Raw load(rsrc_t r, uint32_t row, int it, bool) {
+    Raw o;
+    o.w[0] = bl128(r, row + 32u * (uint32_t)it);
+    o.w[1] = bl128(r, row + 32u * (uint32_t)it + 16u);
+    return o;
+  }
+  template <class XT>
+  static __device__ __forceinline__ float dot(const Raw& w, uint32_t, const uint8_t*, int it, const XT*,
+                                              const XLds& X, bool) {
+    const float4* Xp = (const float4*)X.xf + it * 4;
+    const uint32_t h[8] = {w.w[0].x, w.w[0].y, w.w[0].z, w.w[0].w, w.w[1].x, w.w[1].y, w.w[1].z, w.w[1].w};
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 b = Xp[i];
+      s += f16_bits_to_f32(h[2 * i] & 0xFFFFu) * b.x + f16_bits_to_f32(h[2 * i] >> 16) * b.y +
+           f16_bits_to_f32(h[2 * i + 1] & 0xFFFFu) * b.z + f16_bits_to_f32(h[2 * i + 1] >> 16) * b.w;
     }
     return s;
   }
@@ -681,6 +711,7 @@ static hipError_t pick_types(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
       case T_Q8_0: return pick_lpr<T_Q8_0, T_Q8_0, MODE>(a, s, nb);
       case T_Q5_0: return pick_lpr<T_Q5_0, T_Q5_0, MODE>(a, s, nb);
       case T_F32: return pick_lpr<T_F32, T_F32, MODE>(a, s, nb);
+      case T_F16: return pick_lpr<T_F16, T_F16, MODE>(a, s, nb);
     }
     return hipErrorInvalidValue;
   }
@@ -742,7 +773,7 @@ hipError_t gemv_prepare(size_t bytes) {
   hipError_t e;
   if ((e = prep_types<T_Q4_K, T_Q4_K>(b)) || (e = prep_types<T_Q6_K, T_Q6_K>(b)) ||
       (e = prep_types<T_Q8_0, T_Q8_0>(b)) || (e = prep_types<T_Q5_0, T_Q5_0>(b)) ||
-      (e = prep_types<T_F32, T_F32>(b)) || (e = prep_types<T_Q4_K, T_Q6_K>(b)) || (e = prep_types<T_Q6_K, T_Q4_K>(b)))
+      (e = prep_types<T_F32, T_F32>(b)) || (e = prep_types<T_F16, T_F16>(b)) || (e = prep_types<T_Q4_K, T_Q6_K>(b)) || (e = prep_types<T_Q6_K, T_Q4_K>(b)))
     return e;
   return hipSuccess;
 }

@@ -179,6 +179,20 @@ struct Deq8<T_Q5_0> {  // quant.rs:53-63: the whole 22-byte block, from the dwor
 };
 
 template <>
+struct Deq8<T_F16> {  // a format the reference does not load
+  uint4 a;
+  __device__ __forceinline__ void load(rsrc_t r, uint32_t row, uint32_t k) { a = bl128(r, row + 2 * k); }
+  __device__ __forceinline__ void decode(uint32_t, float (&y)[8]) const {
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      y[2 * i] = f16_bits_to_f32(w[i] & 0xFFFFu);
+      y[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+    }
+  }
+};
+
+template <>
 struct Deq8<T_F32> {
   uint4 a, b;
   __device__ __forceinline__ void load(rsrc_t r, uint32_t row, uint32_t k) {
@@ -298,6 +312,7 @@ static hipError_t gemm_go(const GemmArgs& g, hipStream_t s) {
     case T_Q8_0: hipLaunchKernelGGL((k_gemm_q<T_Q8_0, MODE>), grid, dim3(256), 0, s, g); break;
     case T_Q5_0: hipLaunchKernelGGL((k_gemm_q<T_Q5_0, MODE>), grid, dim3(256), 0, s, g); break;
     case T_F32: hipLaunchKernelGGL((k_gemm_q<T_F32, MODE>), grid, dim3(256), 0, s, g); break;
+    case T_F16: hipLaunchKernelGGL((k_gemm_q<T_F16, MODE>), grid, dim3(256), 0, s, g); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

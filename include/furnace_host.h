@@ -59,8 +59,11 @@ frn_status frn_generate_sampled(frn_ctx* ctx, const uint32_t* prompt, uint32_t n
                                 uint64_t* draws);
 
 /* ---- synthetic models ------------------------------------------------------ */
+/* FRN_MIX_Q4_K_M: Q6_K attn_v / ffn_down on even layers; FRN_MIX_Q4_K_M_LLAMA:
+ * llama.cpp's Q4_K_M rule for them (first and last eighth of the layers and
+ * every third between) */
 enum { FRN_MIX_ALL_Q8_0 = 0, FRN_MIX_Q4_K_M = 1, FRN_MIX_ALL_Q4_K = 2, FRN_MIX_ALL_Q6_K = 3, FRN_MIX_ALL_Q5_0 = 4,
-       FRN_MIX_ALL_F32 = 5 };
+       FRN_MIX_ALL_F32 = 5, FRN_MIX_Q4_K_M_LLAMA = 6, FRN_MIX_ALL_F16 = 7 };
 typedef struct frn_synth_spec {
   uint32_t n_layers, n_heads, n_kv_heads, hidden, ffn, vocab, context_length;
   float rope_theta, rms_eps;

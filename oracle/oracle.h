@@ -45,6 +45,11 @@ int orc_matmul_quant(const float* a, size_t seq, const uint8_t* raw, size_t raw_
 /* tensor.rs:74-80: f32 weights [d_out, d_in] */
 void orc_matmul_f32(const float* a, size_t seq, const float* w, size_t d_out, size_t d_in, float* out);
 
+/* Beyond the reference: F16 tensors widen exactly to f32 in orc_dequantize
+ * (and so load as f32 weights) while switched on; off (the default), F16 is
+ * the reference's "not implemented" error (quant.rs:279). */
+void orc_set_f16_extension(int on);
+
 /* ---- tensor.rs --------------------------------------------------------- */
 float orc_dot(const float* a, const float* b, size_t n);                             /* :146-160 */
 void orc_rmsnorm(const float* x, size_t rows, size_t cols, const float* w, float eps, float* out); /* :164-185 */

@@ -38,6 +38,7 @@ class SamplerState(ctypes.Structure):
 
 _P, _SZ, _U32, _F = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_float
 _SIG = {
+    "orc_set_f16_extension": (None, [ctypes.c_int]),
     "orc_pcg32_seed": (None, [ctypes.POINTER(Pcg32State), ctypes.c_uint64, ctypes.c_uint64]),
     "orc_pcg32_next_u32": (_U32, [ctypes.POINTER(Pcg32State)]),
     "orc_pcg32_next_f32": (_F, [ctypes.POINTER(Pcg32State)]),
@@ -252,6 +253,20 @@ def argmax(x):
 
 def set_threads(n):
     lib().orc_set_threads(int(n))
+
+
+class f16_extension:
+    """Context manager: F16 tensors widen exactly to f32 inside it (the
+    engine's F16 support, which the reference does not have: quant.rs:279);
+    outside it F16 is the reference's "not implemented" error."""
+
+    def __enter__(self):
+        lib().orc_set_f16_extension(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_f16_extension(0)
+        return False
 
 
 class Model:

@@ -140,8 +140,23 @@ static block_fn block_dequant(uint32_t type) { /* quant.rs:137-144 (+ Q8_0) */
   }
 }
 
+/* F16 is not a format the reference loads: its dequantize has no F16 arm
+ * (quant.rs:279).  With the extension switched on (the tests of the
+ * engine's F16 support), F16 data widens exactly to f32 through
+ * orc_f16_to_f32; off, it is the reference's error. */
+static int f16_extension = 0;
+void orc_set_f16_extension(int on) { f16_extension = on != 0; }
+
 /* quant.rs:261-281 dequantize (with the length checks of :17-32, :147-161) */
 int orc_dequantize(uint32_t type, const uint8_t* raw, size_t raw_len, size_t n, float* out) {
+  if (type == ORC_F16 && f16_extension) {
+    if (raw_len != n * 2) {
+      orc_set_error("F16 data is %zu bytes, expected %zu", raw_len, n * 2);
+      return -1;
+    }
+    for (size_t i = 0; i < n; ++i) out[i] = orc_f16_to_f32((uint16_t)(raw[2 * i] | (raw[2 * i + 1] << 8)));
+    return 0;
+  }
   if (type == ORC_F32) {
     if (raw_len != n * 4) {
       orc_set_error("F32 data is %zu bytes, expected %zu", raw_len, n * 4);

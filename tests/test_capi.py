@@ -42,7 +42,7 @@ def test_dequant_validates_before_launch():
 
 def test_matmul_validates_before_launch():
     lib = fa.load()
-    assert lib.frn_matmul_quant(1, None, 0, None, 1, None, 1, 32, None) == 2  # F16: no kernel
+    assert lib.frn_matmul_quant(2, None, 0, None, 1, None, 1, 32, None) == 2  # Q4_0: no kernel
     assert lib.frn_matmul_quant(fa.Q4_K, None, 144, None, 1, None, 1, 100, None) == 3
     assert lib.frn_matmul_quant(fa.Q4_K, None, 100, None, 1, None, 1, 256, None) == 3
     assert b"bad weight byte count" in lib.frn_last_error()

@@ -114,3 +114,22 @@ def test_synthetic_writer_is_deterministic(tmp_path):
     assert open(a, "rb").read() == open(b, "rb").read()
     fa.synth_write(b, seed=4, **kw)
     assert open(a, "rb").read() != open(b, "rb").read()
+
+
+def test_llama_cpp_q4_k_m_layer_mix(tmp_path):
+    # llama.cpp's Q4_K_M (use_more_bits): Q6_K attn_v / ffn_down on layers
+    # i < n/8, i >= 7n/8 and (i - n/8) % 3 == 2; with n = 16 that is
+    # 0, 1, 4, 7, 10, 13, 14, 15
+    path = str(tmp_path / "llama-mix.gguf")
+    fa.synth_write(path, seed=3, n_layers=16, n_heads=2, n_kv_heads=1, hidden=256, ffn=256, vocab=300,
+                   mix=fa.MIX_Q4_K_M_LLAMA, tied=0, embd_type=fa.Q4_K, output_type=fa.Q6_K)
+    m = orc.Model(path)
+    more = {0, 1, 4, 7, 10, 13, 14, 15}
+    for layer in range(16):
+        for name in ("attn_v", "ffn_down"):
+            t, _, _ = m.tensor("blk.%d.%s.weight" % (layer, name))
+            assert t == (fa.Q6_K if layer in more else fa.Q4_K), (layer, name)
+        for name in ("attn_q", "attn_k", "attn_output", "ffn_gate", "ffn_up"):
+            assert m.tensor("blk.%d.%s.weight" % (layer, name))[0] == fa.Q4_K
+    assert m.tensor("output.weight")[0] == fa.Q6_K
+    m.close()

@@ -25,6 +25,13 @@ def small_models():
                                  mix=fa.MIX_ALL_Q5_0, tied=0, embd_type=fa.Q5_0, output_type=fa.Q8_0),
         "tiny-q4_k-gq8": dict(n_layers=2, n_heads=8, n_kv_heads=1, hidden=1024, ffn=768, vocab=500,
                               mix=fa.MIX_ALL_Q4_K, tied=1, embd_type=fa.Q4_K, output_type=fa.Q4_K),
+        # llama.cpp's Q4_K_M layer mix over 16 layers, untied Q6_K output
+        "tiny-llama-q4_k_m": dict(n_layers=16, n_heads=4, n_kv_heads=2, hidden=256, ffn=512, vocab=1500,
+                                  mix=fa.MIX_Q4_K_M_LLAMA, tied=0, embd_type=fa.Q4_K, output_type=fa.Q6_K),
+        # F16 weights (beyond the reference, which rejects them): the oracle
+        # widens them exactly to f32 under its F16 extension
+        "tiny-f16-tied": dict(n_layers=2, n_heads=4, n_kv_heads=2, hidden=256, ffn=512, vocab=1000,
+                              mix=fa.MIX_ALL_F16, tied=1, embd_type=fa.F16, output_type=fa.F16),
     }
 
 
@@ -36,7 +43,11 @@ def test_small_model_prefill_decode(hip, tmpdir_models, name):
     cfg = small_models()[name]
     prompt = rng.integers(0, cfg["vocab"], 300 if name == "tiny-q4_k-gq8" else 9).astype(np.uint32)
     print("model %s prompt %d" % (name, prompt.size), flush=True)
-    ref = orc.Model(path)
+    if cfg["mix"] == fa.MIX_ALL_F16:
+        with orc.f16_extension():
+            ref = orc.Model(path)
+    else:
+        ref = orc.Model(path)
     ref.new_cache(512)
     ref_logits = ref.forward_cached(prompt)
     m = fa.Model(path, max_ctx=512)

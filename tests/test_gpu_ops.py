@@ -48,6 +48,23 @@ def test_dequant_bit_exact(hip, gtype):
         hip.free(d_out)
 
 
+def test_dequant_f16_every_bit_pattern(hip):
+    # F16 (beyond the reference): exact widening, against the oracle's F16
+    # extension, for all 65536 halves
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    d_raw = hip.to_device(bits.view(np.uint8))
+    d_out = hip.malloc(bits.size * 4)
+    fa.dequant_dev(hip, fa.F16, d_raw, bits.size * 2, bits.size, d_out)
+    got = hip.from_device(d_out, bits.size, np.float32)
+    with orc.f16_extension():
+        want = orc.dequantize(orc.F16, bits.tobytes(), bits.size)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    hip.free(d_raw)
+    hip.free(d_out)
+
+
 def test_dequant_reference_known_answers(hip):
     # quant.rs:359-387 Q4_K block through the device path
     b = bytearray(144)
@@ -74,6 +91,8 @@ def _gemv_case(hip, gtype, d_out, d_in, seed, seq=1):
         hip.free(p)
     if gtype == fa.F32:  # F32 weights take tensor::matmul (tensor.rs:74-80)
         return got, orc.matmul_f32(x, raw.view(np.float32).reshape(d_out, d_in))
+    if gtype == fa.F16:  # widened exactly to f32, then as F32 weights
+        return got, orc.matmul_f32(x, raw.view(np.float16).astype(np.float32).reshape(d_out, d_in))
     return got, orc.matmul_quant(x, raw, d_out, d_in, gtype)
 
 
@@ -85,7 +104,8 @@ def _gemv_case(hip, gtype, d_out, d_in, seed, seq=1):
     (fa.Q6_K, 151936, 1536),
     (fa.Q4_K, 256, 1536), (fa.Q6_K, 256, 1536), (fa.Q8_0, 4864, 896), (fa.Q8_0, 896, 4864), (fa.Q8_0, 128, 896),
     (fa.Q4_K, 3584, 18944), (fa.Q6_K, 512, 3584),
-    (fa.Q5_0, 1000, 1536), (fa.Q5_0, 100, 96), (fa.Q8_0, 100, 96), (fa.F32, 300, 512)])
+    (fa.Q5_0, 1000, 1536), (fa.Q5_0, 100, 96), (fa.Q8_0, 100, 96), (fa.F32, 300, 512),
+    (fa.F16, 1536, 1536), (fa.F16, 300, 512), (fa.F16, 100, 96)])
 def test_gemv_within_tolerance(hip, gtype, d_out, d_in):
     got, ref = _gemv_case(hip, gtype, d_out, d_in, seed=d_out * 7 + d_in)
     assert rel_err(got, ref) <= GEMV_TOL

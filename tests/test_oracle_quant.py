@@ -106,6 +106,22 @@ def test_unsupported_type_is_an_error():  # quant.rs:279
         orc.dequantize(orc.F16, b"\x00\x3c", 1)
 
 
+def test_f16_extension_widens_exactly_and_switches_off():
+    # beyond the reference: with the switch on, F16 data widens as numpy's
+    # float16 -> float32 cast does, for every bit pattern (NaNs by class)
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    with orc.f16_extension():
+        got = orc.dequantize(orc.F16, bits.tobytes(), bits.size)
+        with pytest.raises(ValueError, match="expected"):
+            orc.dequantize(orc.F16, bits[:3].tobytes(), 4)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    with pytest.raises(ValueError, match="not implemented"):
+        orc.dequantize(orc.F16, b"\x00\x3c", 1)
+
+
 # ---- f16 widening: every bit pattern against numpy's IEEE conversion ----------
 def test_f16_to_f32_exhaustive():
     bits = np.arange(65536, dtype=np.uint16)

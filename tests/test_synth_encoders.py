@@ -21,6 +21,22 @@ def test_encode_decode_roundtrip(gtype, rel):
     assert np.corrcoef(x, y)[0, 1] > 0.97
 
 
+def test_f16_encoder_rounds_to_nearest_even():
+    # IEEE binary16 round-to-nearest-even, as numpy's float32 -> float16 cast
+    # (normals, subnormals, overflow to inf, signed zero, ties)
+    rng = np.random.default_rng(3)
+    x = np.concatenate([
+        fa.gaussian(12, 0.02, 4096),
+        rng.uniform(-70000, 70000, 1024).astype(np.float32),
+        np.float32(2.0 ** -24) * rng.uniform(-3, 3, 512).astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65520.0, 65519.0, -1e9, 1 + 2 ** -11, 1 + 3 * 2 ** -11], np.float32),
+    ]).astype(np.float32)
+    raw = fa.quantize(fa.F16, x)
+    with np.errstate(over="ignore"):
+        want = x.astype("<f2")
+    assert raw.tobytes() == want.tobytes()
+
+
 def test_gaussian_statistics():
     x = fa.gaussian(5, 0.02, 1 << 18)
     assert abs(x.mean()) < 2e-4 and abs(x.std() - 0.02) < 2e-4
