@@ -50,7 +50,8 @@ class SynthSpec(ctypes.Structure):
                 ("n_layers", "n_heads", "n_kv_heads", "hidden", "ffn", "vocab", "context_length")] + \
                [("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)] + \
                [(n, ctypes.c_uint32) for n in ("mix", "tied", "embd_type", "output_type")] + \
-               [("seed", ctypes.c_uint64), ("weight_std", ctypes.c_float), ("threads", ctypes.c_uint32)]
+               [("seed", ctypes.c_uint64), ("weight_std", ctypes.c_float), ("threads", ctypes.c_uint32),
+                ("alignment", ctypes.c_uint32)]
 
 
 class Timing(ctypes.Structure):

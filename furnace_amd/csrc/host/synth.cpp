@@ -277,6 +277,9 @@ extern "C" frn_status frn_synth_write(const frn_synth_spec* sp, const char* path
   const frn_synth_spec& S = *sp;
   if (!S.n_heads || S.hidden % S.n_heads || !S.n_kv_heads || S.n_heads % S.n_kv_heads)
     return frn_fail(FRN_ESHAPE, "frn_synth_write: bad head configuration");
+  if (S.alignment & (S.alignment - 1))
+    return frn_fail(FRN_EINVAL, "frn_synth_write: alignment %u is not a power of two", S.alignment);
+  const uint64_t align = S.alignment ? S.alignment : 32;
   uint64_t H = S.hidden, hd = H / S.n_heads, qd = H, kd = (uint64_t)S.n_kv_heads * hd, F = S.ffn;
   auto lin_type = [&](int which, uint32_t layer) -> uint32_t {  // which: 0 q,1 k,2 v,3 o,4 gate,5 up,6 down
     switch (S.mix) {
@@ -332,12 +335,13 @@ extern "C" frn_status frn_synth_write(const frn_synth_spec* sp, const char* path
   h.d.insert(h.d.end(), {'G', 'G', 'U', 'F'});
   h.u32(3);
   h.u64(ts.size());
-  uint64_t n_kv = 15 + (S.vocab > 151645 ? 2 : 0);
+  uint64_t n_kv = 15 + (S.vocab > 151645 ? 2 : 0) + (S.alignment ? 1 : 0);
   h.u64(n_kv);
   auto kv_u32 = [&](const char* k, uint32_t v) { h.str(k); h.u32(4); h.u32(v); };
   auto kv_f32 = [&](const char* k, float v) { h.str(k); h.u32(6); h.f32(v); };
   auto kv_str = [&](const char* k, const char* v) { h.str(k); h.u32(8); h.str(v); };
   kv_str("general.architecture", "qwen2");
+  if (S.alignment) kv_u32("general.alignment", S.alignment);
   kv_str("general.name", "furnace-hip synthetic");
   kv_u32("qwen2.block_count", S.n_layers);
   kv_u32("qwen2.context_length", S.context_length);
@@ -382,9 +386,9 @@ extern "C" frn_status frn_synth_write(const frn_synth_spec* sp, const char* path
     t.offset = off;
     t.bytes = tensor_bytes(t.type, t.in * t.out);
     h.u64(off);
-    off += (t.bytes + 31) / 32 * 32;
+    off += (t.bytes + align - 1) / align * align;
   }
-  while (h.d.size() % 32) h.d.push_back(0);
+  while (h.d.size() % align) h.d.push_back(0);
   uint64_t total = h.d.size() + off;
   int fd = ::open(path, O_RDWR | O_CREAT | O_TRUNC, 0644);
   if (fd < 0) return frn_fail(FRN_EINVAL, "cannot create %s", path);

@@ -74,6 +74,9 @@ typedef struct frn_synth_spec {
   uint64_t seed;
   float weight_std;      /* N(0, std) for matrices and biases (0.02) */
   uint32_t threads;      /* 0: all hardware threads */
+  uint32_t alignment;    /* 0: no general.alignment key (32); else a power of
+                            two written as general.alignment, which the tensor
+                            offsets and the data blob then follow */
 } frn_synth_spec;
 /* Writes a GGUF v3 file: qwen2 metadata, tokenizer stubs (vocab strings,
  * types, empty merges, eos 151645 / bos 151643 when in range), norm gains 1.0

@@ -2,6 +2,7 @@
 the hand-assembled file of furnace's src/gguf.rs:532-609 and its negative
 tests (bad magic, truncation), plus the synthetic writer's output."""
 import ctypes
+import os
 import struct
 
 import numpy as np
@@ -133,3 +134,38 @@ def test_llama_cpp_q4_k_m_layer_mix(tmp_path):
             assert m.tensor("blk.%d.%s.weight" % (layer, name))[0] == fa.Q4_K
     assert m.tensor("output.weight")[0] == fa.Q6_K
     m.close()
+
+
+@pytest.mark.parametrize("align", [64, 256, 4096])
+def test_general_alignment_moves_the_data(tmp_path, align):  # gguf.rs:344-354
+    # the same tensors written with the default and with a larger
+    # general.alignment: both loaders must find identical bytes in both
+    # files, at offsets that follow the alignment
+    kw = dict(n_layers=1, n_heads=2, n_kv_heads=1, hidden=256, ffn=288, vocab=70, mix=fa.MIX_ALL_Q5_0, tied=0,
+              embd_type=fa.Q8_0, output_type=fa.Q6_K)
+    a, b = str(tmp_path / "a.gguf"), str(tmp_path / ("b%d.gguf" % align))
+    fa.synth_write(a, seed=9, **kw)
+    fa.synth_write(b, seed=9, alignment=align, **kw)
+    assert os.path.getsize(b) > os.path.getsize(a)
+    names = ["token_embd.weight", "blk.0.attn_q.bias", "blk.0.attn_v.weight", "blk.0.ffn_norm.weight",
+             "blk.0.ffn_down.weight", "output.weight"]
+    ma, mb = orc.Model(a), orc.Model(b)
+    st, g = _open(b)
+    assert st == 0, fa.load().frn_last_error()
+    try:
+        for name in names:
+            ta, mb_t = ma.tensor(name), mb.tensor(name)
+            assert ta[0] == mb_t[0] and ta[1] == mb_t[1] and np.array_equal(ta[2], mb_t[2]), name
+            t, nd, ptr, nb = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_void_p(), ctypes.c_size_t()
+            dims = (ctypes.c_uint64 * 4)()
+            assert fa.load().frn_gguf_tensor(g, name.encode(), ctypes.byref(t), dims, ctypes.byref(nd),
+                                             ctypes.byref(ptr), ctypes.byref(nb)) == 0
+            assert ptr.value % align == 0, name  # the file is mapped at a page boundary
+            got = np.ctypeslib.as_array(ctypes.cast(ptr, ctypes.POINTER(ctypes.c_uint8)), (nb.value,))
+            assert np.array_equal(got, ta[2].view(np.uint8)), name
+    finally:
+        fa.load().frn_gguf_close(g)
+        ma.close()
+        mb.close()
+    with pytest.raises(fa.FrnError, match="power of two"):
+        fa.synth_write(str(tmp_path / "c.gguf"), seed=9, alignment=48, **kw)

@@ -25,9 +25,11 @@ def small_models():
                                  mix=fa.MIX_ALL_Q5_0, tied=0, embd_type=fa.Q5_0, output_type=fa.Q8_0),
         "tiny-q4_k-gq8": dict(n_layers=2, n_heads=8, n_kv_heads=1, hidden=1024, ffn=768, vocab=500,
                               mix=fa.MIX_ALL_Q4_K, tied=1, embd_type=fa.Q4_K, output_type=fa.Q4_K),
-        # llama.cpp's Q4_K_M layer mix over 16 layers, untied Q6_K output
+        # llama.cpp's Q4_K_M layer mix over 16 layers, untied Q6_K output,
+        # general.alignment 256
         "tiny-llama-q4_k_m": dict(n_layers=16, n_heads=4, n_kv_heads=2, hidden=256, ffn=512, vocab=1500,
-                                  mix=fa.MIX_Q4_K_M_LLAMA, tied=0, embd_type=fa.Q4_K, output_type=fa.Q6_K),
+                                  mix=fa.MIX_Q4_K_M_LLAMA, tied=0, embd_type=fa.Q4_K, output_type=fa.Q6_K,
+                                  alignment=256),
         # F16 weights (beyond the reference, which rejects them): the oracle
         # widens them exactly to f32 under its F16 extension
         "tiny-f16-tied": dict(n_layers=2, n_heads=4, n_kv_heads=2, hidden=256, ffn=512, vocab=1000,
