@@ -78,6 +78,7 @@ struct frn_ctx {
   const float* out_norm = nullptr;
   float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *act = nullptr, *logits = nullptr;
   float *part = nullptr, *kcache = nullptr, *vcache = nullptr, *rope = nullptr;
+  float* rope_cur = nullptr;  // the step position's row of `rope`, copied by the embed kernel
   uint64_t* best_part = nullptr;  // per-block argmax candidates of the lm_head kernel
   uint32_t n_best = 0;
   StepState* st = nullptr;
@@ -124,7 +125,7 @@ static void free_ctx(frn_ctx* c) {
   }
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -196,7 +197,8 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
       (e = dmalloc(&x->logits, (size_t)c.vocab * 4)) ||
       (e = dmalloc(&x->part, attention_part_floats(c.n_heads, c.head_dim, c.max_ctx) * 4)) ||
       (e = dmalloc(&x->kcache, kv_bytes)) || (e = dmalloc(&x->vcache, kv_bytes)) ||
-      (e = dmalloc(&x->rope, (size_t)c.max_ctx * c.head_dim * 4)) || (e = dmalloc(&x->st, sizeof(StepState))) ||
+      (e = dmalloc(&x->rope, (size_t)c.max_ctx * c.head_dim * 4)) || (e = dmalloc(&x->rope_cur, c.head_dim * 4)) ||
+      (e = dmalloc(&x->st, sizeof(StepState))) ||
       (e = dmalloc(&x->best_part, ((size_t)c.vocab + 3) / 4 * 8)) ||  // >= lm_head blocks (4+ rows each)
       (e = alloc_prefill(x)) ||
       (e = dmalloc(&x->hist, (size_t)c.max_ctx * 4)) ||
@@ -356,7 +358,8 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
 #define TIMED(cat, call) \
   (tk.rcat >= 0 ? (e = tk.replay(cat, [&]() { return (call); })) : ((e = tk.begin(cat)) ? e : (e = tk.end(call))))
   if (TIMED(CAT_EMBED, launch_embed(c->embd->ptr, c->embd->type, g.hidden,
-                                    (uint32_t)type_row_bytes(c->embd->type, g.hidden), c->st, c->x, s)))
+                                    (uint32_t)type_row_bytes(c->embd->type, g.hidden), c->st, c->x, c->rope,
+                                    g.head_dim, c->rope_cur, s)))
     return e;
   auto seg = [&](const DevTensor* w, const DevTensor* w2, const float* bias, float* out, const float* resid) {
     GemvSeg sg{};
@@ -393,7 +396,7 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
     // rope, KV append, attention (model.rs:460-467)
     size_t lo = (size_t)l * g.max_ctx * g.n_kv_heads * g.head_dim;
     const uint32_t cap = c->rec_long ? ATTENTION_MAX_SPLITS_LONG : ATTENTION_MAX_SPLITS;
-    if (TIMED(CAT_ATTN, launch_attention(c->q, c->k, c->v, c->rope, c->kcache + lo, c->vcache + lo, g.n_heads,
+    if (TIMED(CAT_ATTN, launch_attention(c->q, c->k, c->v, c->rope_cur, c->kcache + lo, c->vcache + lo, g.n_heads,
                                          g.n_kv_heads, g.head_dim, g.max_ctx, scale, c->part, c->st, cap, s)))
       return e;
     if (c->rec_long) {
@@ -879,6 +882,8 @@ extern "C" frn_status frn_bench_kernel(frn_ctx* c, const char* name, uint32_t la
   if (cat < 0) return fail(FRN_EINVAL, "frn_bench_kernel: no kernel category '%s'", name);
   if (layer != FRN_ALL_LAYERS && layer >= c->cfg.n_layers)
     return fail(FRN_EINVAL, "frn_bench_kernel: layer %u out of range", layer);
+  // the replayed kernels run a step at position len (and write its KV row)
+  if (frn_status st = check_ready(c, 1)) return st;
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
   hipEvent_t e0, e1;
   HIP_TRY(hipEventCreate(&e0), "hipEventCreate");

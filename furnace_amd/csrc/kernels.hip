@@ -780,8 +780,10 @@ hipError_t gemv_prepare(size_t bytes) {
 
 // ---- embedding row (model.rs:482-506) --------------------------------------
 __global__ void k_embed(const uint8_t* __restrict__ table, uint32_t type, uint32_t hidden, uint32_t row_bytes,
-                        StepState* st, float* __restrict__ x) {
+                        StepState* st, float* __restrict__ x, const float* __restrict__ rope, uint32_t hd,
+                        float* __restrict__ rope_cur) {
   uint32_t tok = st->tok;
+  if (blockIdx.x == 0 && threadIdx.x < hd) rope_cur[threadIdx.x] = rope[(size_t)st->pos * hd + threadIdx.x];
   const uint8_t* row = table + (size_t)tok * row_bytes;
   int be = blk_elems(type), bb = blk_bytes(type);
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
@@ -789,8 +791,10 @@ __global__ void k_embed(const uint8_t* __restrict__ table, uint32_t type, uint32
 }
 
 hipError_t launch_embed(const uint8_t* table, uint32_t type, uint32_t hidden, uint32_t row_bytes, StepState* st,
-                        float* x, hipStream_t s) {
-  hipLaunchKernelGGL(k_embed, dim3((hidden + 255) / 256), dim3(256), 0, s, table, type, hidden, row_bytes, st, x);
+                        float* x, const float* rope, uint32_t hd, float* rope_cur, hipStream_t s) {
+  if (hd > 256) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_embed, dim3((hidden + 255) / 256), dim3(256), 0, s, table, type, hidden, row_bytes, st, x, rope,
+                     hd, rope_cur);
   return hipGetLastError();
 }
 
@@ -799,9 +803,10 @@ hipError_t launch_embed(const uint8_t* table, uint32_t type, uint32_t hidden, ui
 // positions (attention_split_len(pos + 1) of them, in sub-tiles of 64) for
 // the GQ query heads sharing g:
 //  - rotates those query heads and head g's new key at the step position
-//    (rope_cs holds cos[hd/2] | sin[hd/2] per position, computed on the host
-//    with the CPU path's powf/sinf/cosf; the rotation is evaluated without
-//    FMA contraction, so q/k match the CPU bit for bit given equal inputs);
+//    (cs holds cos[hd/2] | sin[hd/2] of that position, the row the embed
+//    kernel copied from the host-computed table, made with the CPU path's
+//    powf/sinf/cosf; the rotation is evaluated without FMA contraction, so
+//    q/k match the CPU bit for bit given equal inputs);
 //  - the block holding the step position appends head g's k/v to the cache;
 //  - per sub-tile: scores from K rows in registers, softmax with the
 //    running max and sum of the split, P.V from V rows in LDS; the next
@@ -858,6 +863,14 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     rb[r] = src[j + HALF];
   }
   const float vnew = vn[(size_t)g * HD + (threadIdx.x % HD)];
+#pragma unroll
+  for (int r = 0; r < RR; ++r) {
+    int i = threadIdx.x + 256 * r;
+    if (i >= GQ * HALF + HALF) i = 0;
+    const int j = i % HALF;
+    rc[r] = cs[j];
+    rs[r] = cs[HALF + j];
+  }
   const uint32_t pos = st->pos, T = pos + 1;
   const uint32_t len = attention_split_len(T, cap), t0 = split * len;
   if (t0 >= T) return;
@@ -874,15 +887,6 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     }
   };
   if (len != C) load_tile(0);  // longer splits: the first sub-tile starts elsewhere
-  const float* cr = cs + (size_t)pos * HD;
-#pragma unroll
-  for (int r = 0; r < RR; ++r) {
-    int i = threadIdx.x + 256 * r;
-    if (i >= GQ * HALF + HALF) i = 0;
-    const int j = i % HALF;
-    rc[r] = cr[j];
-    rs[r] = cr[HALF + j];
-  }
 #pragma unroll
   for (int r = 0; r < RR; ++r) {
     const int i = threadIdx.x + 256 * r;

@@ -57,8 +57,10 @@ hipError_t gemv_prepare(size_t max_lds_bytes);  // raises dynamic-LDS limits onc
 // Blocks launch_gemv uses for a single segment of `rows` rows and in `in`.
 uint32_t gemv_blocks(uint32_t type, uint32_t rows, uint32_t in);
 
+// Embedding row of st->tok into x; also copies row st->pos of the RoPE
+// table (hd floats, cos | sin) to rope_cur for the step's attention launches.
 hipError_t launch_embed(const uint8_t* table, uint32_t type, uint32_t hidden, uint32_t row_bytes, StepState* st,
-                        float* x, hipStream_t s);
+                        float* x, const float* rope, uint32_t hd, float* rope_cur, hipStream_t s);
 constexpr uint32_t ATTENTION_CHUNK = 64;  // positions per attention sub-tile
 // At most 16 splits while the o-proj GEMV merges them in its staging
 // (GEMV_RESID_ATT: one or two batches of loads); at most 64 in the
@@ -67,11 +69,12 @@ constexpr uint32_t ATTENTION_MAX_SPLITS = 16;
 constexpr uint32_t ATTENTION_MAX_SPLITS_LONG = 64;
 // Steps over more positions than this (pos + 1) run the long-context form.
 constexpr uint32_t ATTENTION_LONG_FROM = 1024;
-// RoPE(q), RoPE(k) at the step's position, KV-cache append and
-// split-sequence GQA attention in one launch, with at most `cap` splits;
+// RoPE(q), RoPE(k) at the step's position (rope_cur: that position's
+// cos | sin row), KV-cache append and split-sequence GQA attention in one
+// launch, with at most `cap` splits;
 // writes the per-split partials that a GEMV_RESID_ATT launch (cap 16) or
 // launch_attn_merge (cap 64) merges (layout in GemvArgs).
-hipError_t launch_attention(const float* q, const float* k, const float* v, const float* rope_cs, float* k_cache,
+hipError_t launch_attention(const float* q, const float* k, const float* v, const float* rope_cur, float* k_cache,
                             float* v_cache, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                             uint32_t max_ctx, float scale, float* part, const StepState* st, uint32_t cap,
                             hipStream_t s);
