@@ -174,14 +174,27 @@ struct XF {
   float s;
 };
 
+// Padded f32 layout (the f32 form, Q4_K/Q6_K items): float4 f of x sits at
+// f + f/16 + 4 (f/64), one spare slot after every 4 chunks of 16 values and
+// four more after every 16.  The lanes of one LDS cycle read chunks 16b +
+// 4j + h (Q4_K: j < 4, h < 2, two consecutive b) or 16k + 8h + 2p + l
+// (Q6_K): unpadded, those sit at 4 (resp. 4) distinct 16-byte slots of a
+// 256-byte bank row, 8-way (4-way) conflicts; padded, at 16 distinct slots
+// (Q4_K) and 2-way at most (Q6_K).  A chunk's 4 float4 stay contiguous.
+__host__ __device__ constexpr uint32_t xf_pad4(uint32_t f) { return f + (f >> 4) + 4u * (f >> 6); }
+// floats the padded layout of K values occupies (K a multiple of 4)
+__host__ __device__ constexpr uint32_t xf_padded_floats(uint32_t K) { return K + K / 8; }
+
 struct XLds {
-  const float* xf;     // [K]
+  const float* xf;     // [K] (PAD: padded as xf_pad4)
   const uint8_t* pl;   // int8 form: 4 planes of K bytes; f32 form: K/16 chunk sums
   uint32_t K;
+  template <bool PAD = false>
   __device__ __forceinline__ XF fchunk(uint32_t c) const {
     XF x;
+    const uint32_t b = PAD ? xf_pad4(4u * c) : 4u * c;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x.v[i] = ((const float4*)xf)[4 * c + i];
+    for (int i = 0; i < 4; ++i) x.v[i] = ((const float4*)xf)[b + i];
     x.s = ((const float*)pl)[c];
     return x;
   }

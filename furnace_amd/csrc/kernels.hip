@@ -192,7 +192,7 @@ struct Fmt<T_F16> {  // 16 halves per item (a format the reference does not load
 __device__ __forceinline__ float4 u4f(uint4 v) {
   return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
 }
-template <int NX, bool NORM, bool ATT, bool DIG>
+template <int NX, bool NORM, bool ATT, bool DIG, bool PAD = false>
 struct XStage {
   // ATT: x is the attention output, merged here from the per-split partials
   // (o, m, l) of the attention kernel: NB splits are loaded up front with
@@ -330,8 +330,9 @@ struct XStage {
         b.x = b.x * inv * wb.x; b.y = b.y * inv * wb.y; b.z = b.z * inv * wb.z; b.w = b.w * inv * wb.w;
       }
       if (live) {
-        ((float4*)xf)[2 * u] = a;
-        ((float4*)xf)[2 * u + 1] = b;
+        const uint32_t f = PAD ? xf_pad4(2 * u) : 2 * u;  // 2u, 2u + 1 share a chunk
+        ((float4*)xf)[f] = a;
+        ((float4*)xf)[f + 1] = b;
       }
       if (!DIG) {
         float s16 = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
@@ -421,6 +422,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   // gate_up 9.9 vs 11.3 and o_proj 6.2 vs 6.7 us in favour of the digits.
   constexpr bool DIG = NX <= 2;
   using XT = typename std::conditional<DIG, XC, XF>::type;
+  // the f32 form stages x padded (xf_pad4) for the K-quant items while the
+  // padded x leaves room for 2 blocks per CU (in <= 10240, NX <= 5)
+  constexpr bool PAD = !DIG && NX <= 5 && (T == T_Q4_K || T == T_Q6_K);
   // the wave index through readfirstlane: the compiler then knows every
   // per-wave quantity below is uniform (scalar loop control, no exec masks)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -436,7 +440,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   const rsrc_t rex = make_rsrc(exp_, exp_ ? sg.rows * 4 : 0);
   const XLds X{xf, pl, a.in};
 
-  XStage<NX, NORM, ATT, DIG> xs;
+  XStage<NX, NORM, ATT, DIG, PAD> xs;
   const rsrc_t rp = make_rsrc(a.att_part, ATT ? a.att_part_bytes : 0);
   if (ATT)
     xs.load_att(a, rp);
@@ -507,7 +511,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
       if constexpr (DIG)
         xc[i] = X.chunk(F::chunk(itc, i, pr));
       else
-        xc[i] = X.fchunk(F::chunk(itc, i, pr));
+        xc[i] = X.template fchunk<PAD>(F::chunk(itc, i, pr));
     }
   };
 
@@ -586,9 +590,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
   extern __shared__ float4 smem4[];
   __shared__ float red4[4];
   __shared__ uint64_t best_s[4];
-  // LDS: x[in] f32 | 4 byte planes of in bytes (digits, metadata)
+  // LDS: x[in] f32 | 4 byte planes of in bytes (digits, metadata); the f32
+  // form: x (padded as xf_pad4 room for NX <= 5) | the in/16 chunk sums
   float* xf = (float*)smem4;
-  uint8_t* pl = (uint8_t*)(xf + a.in);
+  uint8_t* pl = (uint8_t*)(xf + (NX > 2 && NX <= 5 ? xf_padded_floats(a.in) : a.in));
   int si = 0;
   while (si + 1 < a.n_seg && blockIdx.x >= a.seg[si + 1].block0) ++si;
   const GemvSeg& sg = a.seg[si];
@@ -601,8 +606,12 @@ __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
 }
 
 // LDS of a launch: x as f32, then the int8 form's 4 planes of `in` bytes
-// (in <= 4096) or the f32 form's in/16 chunk sums.
-size_t gemv_lds_bytes(uint32_t in, bool) { return (size_t)in * (in <= 4096 ? 8 : 4) + in / 4; }
+// (in <= 4096), or the f32 form's in/16 chunk sums after x, padded for
+// in <= 10240.
+size_t gemv_lds_bytes(uint32_t in, bool) {
+  if (in <= 4096) return (size_t)in * 8 + in / 4;
+  return (size_t)(in <= 10240 ? xf_padded_floats(in) : in) * 4 + in / 4;
+}
 
 
 // Lanes per row: the choice in {16, 32, 64} with the shortest critical
@@ -674,15 +683,18 @@ static hipError_t go(GemvArgs a, hipStream_t s, uint32_t* nblocks) {
 }
 
 // in <= 4096 (the hidden-size inputs, with or without rmsnorm) or, without
-// rmsnorm and only for STORE/RESID, in <= 20480 (the FFN down projection).
+// rmsnorm and only for STORE/RESID, in <= 20480 (the FFN down projection;
+// NX 5 up to 10240, whose padded x stays under 64 KiB of LDS, NX 10 above).
 template <uint32_t T0, uint32_t T1, int MODE, int LPR>
 static hipError_t pick_nx(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
   const int n_items = items_per_row(T0, a.in, ((a.in / 32) % 2) == 0);
   const bool one = n_items <= LPR * gemv_bi(T0, MODE);  // one step per unit
   if (a.in <= 2048) return one ? go<T0, T1, LPR, MODE, 1, true>(a, s, nb) : go<T0, T1, LPR, MODE, 1, false>(a, s, nb);
   if (a.in <= 4096) return one ? go<T0, T1, LPR, MODE, 2, true>(a, s, nb) : go<T0, T1, LPR, MODE, 2, false>(a, s, nb);
-  if constexpr (MODE == GEMV_STORE || MODE == GEMV_RESID)
+  if constexpr (MODE == GEMV_STORE || MODE == GEMV_RESID) {
+    if (a.norm_w == nullptr && a.in <= 10240) return go<T0, T1, LPR, MODE, 5, false>(a, s, nb);
     if (a.norm_w == nullptr && a.in <= 20480) return go<T0, T1, LPR, MODE, 10, false>(a, s, nb);
+  }
   return hipErrorInvalidValue;
 }
 
