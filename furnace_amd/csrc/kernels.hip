@@ -594,11 +594,16 @@ __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
   // form: x (padded as xf_pad4 room for NX <= 5) | the in/16 chunk sums
   float* xf = (float*)smem4;
   uint8_t* pl = (uint8_t*)(xf + (NX > 2 && NX <= 5 ? xf_padded_floats(a.in) : a.in));
+  // Only STORE launches carry several segments (launch_gemv checks): the
+  // other modes read segment 0's fields at constant offsets, in the same
+  // round trip as the rest of the arguments, not after a segment search.
+  constexpr bool ONESEG = MODE != GEMV_STORE;
   int si = 0;
-  while (si + 1 < a.n_seg && blockIdx.x >= a.seg[si + 1].block0) ++si;
-  const GemvSeg& sg = a.seg[si];
-  const uint32_t blk = blockIdx.x - sg.block0;
-  const uint32_t nblk = (si + 1 < a.n_seg ? a.seg[si + 1].block0 : gridDim.x) - sg.block0;
+  if constexpr (!ONESEG)
+    while (si + 1 < a.n_seg && blockIdx.x >= a.seg[si + 1].block0) ++si;
+  const GemvSeg& sg = a.seg[ONESEG ? 0 : si];
+  const uint32_t blk = ONESEG ? blockIdx.x : blockIdx.x - sg.block0;
+  const uint32_t nblk = ONESEG ? gridDim.x : (si + 1 < a.n_seg ? a.seg[si + 1].block0 : gridDim.x) - sg.block0;
   if (T0 == T1 || sg.type == T0)
     gemv_body<T0, LPR, MODE, NX, NORM, ONE>(a, sg, blk, nblk, xf, pl, red4, best_s);
   else
@@ -747,6 +752,7 @@ static hipError_t launch_split(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
 }
 
 hipError_t launch_gemv(GemvArgs a, GemvMode mode, hipStream_t s, uint32_t* nb) {
+  if (a.n_seg < 1 || a.n_seg > 3 || (mode != GEMV_STORE && a.n_seg != 1)) return hipErrorInvalidValue;
   for (int i = 0; i < a.n_seg; ++i)  // buffer offsets are 32-bit with BUF_INVALID above the range
     if ((uint64_t)a.seg[i].rows * a.seg[i].row_bytes >= BUF_INVALID) return hipErrorInvalidValue;
   switch (mode) {
