@@ -56,11 +56,12 @@ __host__ __device__ inline int items_per_row(uint32_t t, uint32_t in, bool pairs
   return (int)(in / 16);  // F32, F16: 16 values per item
 }
 
-// Items of one row a lane loads per pipeline step: 3 for the K-quants, 2
-// for the others, one less for SWIGLU (two rows per lane) to stay within
-// the registers of 2 blocks per CU.
+// Items of one row a lane loads per pipeline step: 3 for the K-quants (also
+// for SWIGLU's two rows per lane: 248 VGPRs, still 2 blocks per CU; 16
+// lanes x 3 items cover a 1536-value row exactly, where 32 x 2 left a
+// quarter of the slots masked), 2 for the others, one less for SWIGLU.
 __host__ __device__ constexpr int gemv_bi(uint32_t t, int mode) {
-  return (t == T_Q4_K || t == T_Q6_K ? 3 : 2) - (mode == GEMV_SWIGLU ? 1 : 0);
+  return t == T_Q4_K || t == T_Q6_K ? 3 : 2 - (mode == GEMV_SWIGLU ? 1 : 0);
 }
 
 // Per-format raw-register type, the NC staged chunks an item reads
