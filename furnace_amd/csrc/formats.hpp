@@ -105,6 +105,19 @@ __device__ __forceinline__ void q4k_scale_min_regs(uint32_t a, uint32_t b, uint3
   sc = j < 4 ? sc_lo : sc_hi;
   m = j < 4 ? m_lo : m_hi;
 }
+// The scale and min of sub-blocks 2*j64 and 2*j64 + 1 (one Q4_K item's
+// pair, both below 4 or both from 4 on) packed as bytes 0 and 1 of sc and
+// m: bytes t, t+1 (t = 2*(j64 & 1)) of the 6-bit fields, or of the 4-bit
+// fields of s8..11 with the top 2 bits of s0..7 above them.  Every mask
+// and shift depends on the lane's j64 only.
+__device__ __forceinline__ void q4k_scale_min_pair(uint32_t a, uint32_t b, uint32_t c, int j64, uint32_t& sc,
+                                                   uint32_t& m) {
+  const uint32_t s = 16u * (uint32_t)(j64 & 1);
+  const bool hi = j64 >= 2;
+  const uint32_t mask1 = hi ? 0x0F0Fu : 0x3F3Fu, mask2 = hi ? 0xC0C0u : 0u, msh = hi ? 4u : 0u;
+  sc = (((hi ? c : a) >> s) & mask1) | (((a >> s) & mask2) >> 2);
+  m = (((hi ? c : b) >> (s + msh)) & mask1) | (((b >> s) & mask2) >> 2);
+}
 
 // Value i of one block (quant.rs:17-42, 53-63, 93-109, 114-133).
 __device__ __forceinline__ float decode_elem(uint32_t t, const uint8_t* b, int i) {
@@ -308,9 +321,9 @@ __device__ __forceinline__ uint32_t q4k_chunk(int item, int i) {
 __device__ __forceinline__ float q4k_dot(const Q4KRaw& r, int item, const XC& xA, const XC& xB) {
   int j = item & 7, j64 = j >> 1;
   float d = f16_bits_to_f32(r.hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(r.hdr.x >> 16);
-  uint32_t scA, mA, scB, mB;  // scales[12] live in hdr.y..hdr.w
-  q4k_scale_min_regs(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j64, scA, mA);
-  q4k_scale_min_regs(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j64 + 1, scB, mB);
+  uint32_t sc, m;  // scales[12] live in hdr.y..hdr.w
+  q4k_scale_min_pair(r.hdr.y, r.hdr.z, r.hdr.w, j64, sc, m);
+  const uint32_t scA = sc & 0xFFu, scB = (sc >> 8) & 0xFFu, mA = m & 0xFFu, mB = (m >> 8) & 0xFFu;
   uint32_t lo[4] = {r.q.x & 0x0F0F0F0Fu, r.q.y & 0x0F0F0F0Fu, r.q.z & 0x0F0F0F0Fu, r.q.w & 0x0F0F0F0Fu};
   uint32_t hi[4] = {(r.q.x >> 4) & 0x0F0F0F0Fu, (r.q.y >> 4) & 0x0F0F0F0Fu, (r.q.z >> 4) & 0x0F0F0F0Fu,
                     (r.q.w >> 4) & 0x0F0F0F0Fu};
@@ -346,9 +359,9 @@ __device__ __forceinline__ float sx16(const uint32_t* w, const XF& x) {
 __device__ __forceinline__ float q4k_dot(const Q4KRaw& r, int item, const XF& xA, const XF& xB) {
   int j = item & 7, j64 = j >> 1;
   float d = f16_bits_to_f32(r.hdr.x & 0xFFFFu), dmin = f16_bits_to_f32(r.hdr.x >> 16);
-  uint32_t scA, mA, scB, mB;
-  q4k_scale_min_regs(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j64, scA, mA);
-  q4k_scale_min_regs(r.hdr.y, r.hdr.z, r.hdr.w, 2 * j64 + 1, scB, mB);
+  uint32_t sc, m;
+  q4k_scale_min_pair(r.hdr.y, r.hdr.z, r.hdr.w, j64, sc, m);
+  const uint32_t scA = sc & 0xFFu, scB = (sc >> 8) & 0xFFu, mA = m & 0xFFu, mB = (m >> 8) & 0xFFu;
   uint32_t lo[4] = {r.q.x & 0x0F0F0F0Fu, r.q.y & 0x0F0F0F0Fu, r.q.z & 0x0F0F0F0Fu, r.q.w & 0x0F0F0F0Fu};
   uint32_t hi[4] = {(r.q.x >> 4) & 0x0F0F0F0Fu, (r.q.y >> 4) & 0x0F0F0F0Fu, (r.q.z >> 4) & 0x0F0F0F0Fu,
                     (r.q.w >> 4) & 0x0F0F0F0Fu};
