@@ -157,13 +157,16 @@ __device__ __forceinline__ float decode_elem(uint32_t t, const uint8_t* b, int i
 
 // ---- activation vector in LDS ----------------------------------------------
 // A GEMV block stages its input vector once:
-//   xf[K]     f32 values (rmsnorm applied), used by the f32 items;
+//   xf[K]     f32 values (rmsnorm applied), used by the f32 items (not
+//             written where only K-quant items read the int8 form);
 //   4 planes of K/16 records of 16 bytes, one record per 16-value chunk c:
 //     plane 0..2: the chunk's digits d0, d1, d2 (signed bytes) with
-//                 x ~= s * (d0 + d1/128 + d2/16384) per 32-value chunk
-//                 (|error| <= max|x| * 2^-22 -- f32-level);
+//                 x ~= s * (d0 + d1/128 + d2/16384) per 32-value chunk,
+//                 s = 1/(127/max|x|) through hardware reciprocals
+//                 (|error| <= max|x| * 2^-21 -- f32-level);
 //     plane 3:    {s / 16384, sum(x), -32*sum(d0), -32*(128*sum(d1) + sum(d2))}
-//                 (the digit sums pre-multiplied by Q6_K's -32 offset).
+//                 (the digit sums pre-multiplied by Q6_K's -32 offset; 0
+//                 where only Q4_K or Q8_0 items read the record).
 // Records sit at chunk index swz(c), a permutation that spreads the chunks
 // a 16-lane group reads in one instruction over the LDS banks.
 // (Only whole groups of 8 chunks are permuted, so the map stays inside the

@@ -193,7 +193,11 @@ struct Fmt<T_F16> {  // 16 halves per item (a format the reference does not load
 __device__ __forceinline__ float4 u4f(uint4 v) {
   return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
 }
-template <int NX, bool NORM, bool ATT, bool DIG, bool PAD = false>
+// XF: the items read the f32 copy of x (every format but the K-quants in
+// the int8 form); DSUM: they read the chunks' digit sums (Q6_K and the
+// formats not known to skip them; Q4_K and Q8_0 read only the chunk
+// scale and sum(x)).
+template <int NX, bool NORM, bool ATT, bool DIG, bool PAD = false, bool XF = true, bool DSUM = true>
 struct XStage {
   // ATT: x is the attention output, merged here from the per-split partials
   // (o, m, l) of the attention kernel: NB splits are loaded up front with
@@ -330,7 +334,7 @@ struct XStage {
         a.x = a.x * inv * wa.x; a.y = a.y * inv * wa.y; a.z = a.z * inv * wa.z; a.w = a.w * inv * wa.w;
         b.x = b.x * inv * wb.x; b.y = b.y * inv * wb.y; b.z = b.z * inv * wb.z; b.w = b.w * inv * wb.w;
       }
-      if (live) {
+      if (live && (XF || !DIG)) {
         const uint32_t f = PAD ? xf_pad4(2 * u) : 2 * u;  // 2u, 2u + 1 share a chunk
         ((float4*)xf)[f] = a;
         ((float4*)xf)[f + 1] = b;
@@ -349,8 +353,10 @@ struct XStage {
         xsum += v[j];
       }
       amax = group_reduce<4>(amax, OpMax());  // over the 32-value chunk
-      const float inv_s = amax > 0.f ? 127.0f / amax : 0.f;
-      const float cs = amax > 0.f ? (1.0f / inv_s) * (1.0f / 16384.0f) : 0.f;
+      // hardware reciprocals: the digits only need cs * inv_s = 2^-14 to
+      // f32 precision, not correctly rounded quotients
+      const float inv_s = amax > 0.f ? 127.0f * __builtin_amdgcn_rcpf(amax) : 0.f;
+      const float cs = amax > 0.f ? __builtin_amdgcn_rcpf(inv_s) * (1.0f / 16384.0f) : 0.f;
       uint32_t w0[2] = {0, 0}, w1[2] = {0, 0}, w2[2] = {0, 0};
       int s0 = 0, s1 = 0, s2 = 0;
 #pragma unroll
@@ -369,9 +375,11 @@ struct XStage {
       }
       // per 16-value record: the two threads u, u^1
       xsum = group_reduce<2>(xsum);
-      s0 = group_reduce<2>(s0);
-      s1 = group_reduce<2>(s1);
-      s2 = group_reduce<2>(s2);
+      if (DSUM) {
+        s0 = group_reduce<2>(s0);
+        s1 = group_reduce<2>(s1);
+        s2 = group_reduce<2>(s2);
+      }
       if (live) {
         const uint32_t c = u >> 1, off = 16u * swz(c, n16) + 8u * (u & 1);
         *(uint2*)(pl + off) = make_uint2(w0[0], w0[1]);
@@ -379,7 +387,8 @@ struct XStage {
         *(uint2*)(pl + 2 * K + off) = make_uint2(w2[0], w2[1]);
         if ((u & 1) == 0)
           *(float4*)(pl + 3 * K + 16u * swz(c, n16)) =
-              make_float4(cs, xsum, __int_as_float(-32 * s0), __int_as_float(-32 * (128 * s1 + s2)));
+              make_float4(cs, xsum, DSUM ? __int_as_float(-32 * s0) : 0.f,
+                          DSUM ? __int_as_float(-32 * (128 * s1 + s2)) : 0.f);
       }
     }
     __syncthreads();
@@ -441,7 +450,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   const rsrc_t rex = make_rsrc(exp_, exp_ ? sg.rows * 4 : 0);
   const XLds X{xf, pl, a.in};
 
-  XStage<NX, NORM, ATT, DIG, PAD> xs;
+  XStage<NX, NORM, ATT, DIG, PAD, !(T == T_Q4_K || T == T_Q6_K), !(T == T_Q4_K || T == T_Q8_0)> xs;
   const rsrc_t rp = make_rsrc(a.att_part, ATT ? a.att_part_bytes : 0);
   if (ATT)
     xs.load_att(a, rp);
