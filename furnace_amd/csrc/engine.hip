@@ -400,7 +400,7 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
                                          g.n_kv_heads, g.head_dim, g.max_ctx, scale, c->part, c->st, cap, s)))
       return e;
     if (c->rec_long) {
-      // long contexts: up to 64 splits, merged once (model.rs:436-438),
+      // long contexts: up to 128 splits, merged once (model.rs:436-438),
       // then o-proj + residual on the merged rows (model.rs:469-470)
       if (TIMED(CAT_ATTN, launch_attn_merge(c->part, c->att, g.n_heads, g.head_dim, g.max_ctx, c->st, s))) return e;
       GemvArgs o = args(QD, c->att, nullptr);

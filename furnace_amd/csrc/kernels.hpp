@@ -63,17 +63,18 @@ hipError_t launch_embed(const uint8_t* table, uint32_t type, uint32_t hidden, ui
                         float* x, const float* rope, uint32_t hd, float* rope_cur, hipStream_t s);
 constexpr uint32_t ATTENTION_CHUNK = 64;  // positions per attention sub-tile
 // At most 16 splits while the o-proj GEMV merges them in its staging
-// (GEMV_RESID_ATT: one or two batches of loads); at most 64 in the
-// long-context step, whose splits k_attn_merge merges once.
+// (GEMV_RESID_ATT: one or two batches of loads); at most 128 in the
+// long-context step, whose splits k_attn_merge merges once (one 64-position
+// sub-tile per block up to 8192 positions).
 constexpr uint32_t ATTENTION_MAX_SPLITS = 16;
-constexpr uint32_t ATTENTION_MAX_SPLITS_LONG = 64;
+constexpr uint32_t ATTENTION_MAX_SPLITS_LONG = 128;
 // Steps over more positions than this (pos + 1) run the long-context form.
 constexpr uint32_t ATTENTION_LONG_FROM = 1024;
 // RoPE(q), RoPE(k) at the step's position (rope_cur: that position's
 // cos | sin row), KV-cache append and split-sequence GQA attention in one
 // launch, with at most `cap` splits;
 // writes the per-split partials that a GEMV_RESID_ATT launch (cap 16) or
-// launch_attn_merge (cap 64) merges (layout in GemvArgs).
+// launch_attn_merge (cap 128) merges (layout in GemvArgs).
 hipError_t launch_attention(const float* q, const float* k, const float* v, const float* rope_cur, float* k_cache,
                             float* v_cache, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                             uint32_t max_ctx, float scale, float* part, const StepState* st, uint32_t cap,
@@ -82,7 +83,7 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, cons
 // e^(m_s - M) l_s over the step's splits, one block per query head.
 hipError_t launch_attn_merge(const float* part, float* out, uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx,
                              const StepState* st, hipStream_t s);
-// partials buffer: n_heads x attention_splits(max_ctx, 64) x (head_dim + 2)
+// partials buffer: n_heads x attention_splits(max_ctx, 128) x (head_dim + 2)
 size_t attention_part_floats(uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx);
 // the most splits a step can have with at most `cap` (att_ms for cap 16)
 uint32_t attention_splits(uint32_t max_ctx, uint32_t cap = ATTENTION_MAX_SPLITS);
