@@ -103,8 +103,8 @@ struct frn_ctx {
   uint32_t last_next = 0xFFFFFFFFu;
   bool finalized = false, have_logits = false;
   // captured steps: [0] short contexts, [1] past ATTENTION_LONG_FROM positions
-  hipGraphExec_t g_step[2] = {}, g_prefill[2] = {};
-  hipGraph_t graph_step[2] = {}, graph_prefill[2] = {};
+  hipGraphExec_t g_step[2] = {}, g_prefill[2] = {}, g_multi[2] = {};
+  hipGraph_t graph_step[2] = {}, graph_prefill[2] = {}, graph_multi[2] = {};
   bool rec_long = false;  // the form record_step records (long-context attention)
   float* att = nullptr;   // [n_heads * head_dim] merged attention output (long-context form)
   // --timings: the step runs eagerly with an event pair around each kernel
@@ -122,6 +122,8 @@ static void free_ctx(frn_ctx* c) {
     if (c->g_prefill[i]) (void)hipGraphExecDestroy(c->g_prefill[i]);
     if (c->graph_step[i]) (void)hipGraphDestroy(c->graph_step[i]);
     if (c->graph_prefill[i]) (void)hipGraphDestroy(c->graph_prefill[i]);
+    if (c->g_multi[i]) (void)hipGraphExecDestroy(c->g_multi[i]);
+    if (c->graph_multi[i]) (void)hipGraphDestroy(c->graph_multi[i]);
   }
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -146,6 +148,8 @@ constexpr uint32_t PREFILL_ROWS = 256;
 // frn_decode_greedy's steps per host synchronisation (and the most steps
 // that run past a stop id before the host sees it).
 constexpr uint32_t GREEDY_BATCH = 32;
+// decode steps per captured multi-step graph of frn_decode_greedy
+constexpr uint32_t GREEDY_MULTI = 4;
 
 static hipError_t alloc_prefill(frn_ctx* x) {
   const frn_config& c = x->cfg;
@@ -454,10 +458,12 @@ static hipError_t timed_step(frn_ctx* c, bool with_logits) {
   return hipSuccess;
 }
 
-static frn_status capture(frn_ctx* c, bool with_logits, hipGraph_t* graph, hipGraphExec_t* exec) {
+static frn_status capture(frn_ctx* c, bool with_logits, hipGraph_t* graph, hipGraphExec_t* exec,
+                          uint32_t steps = 1) {
   HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
   Tick tk{c, false};
-  hipError_t e = record_step(c, with_logits, tk);
+  hipError_t e = hipSuccess;
+  for (uint32_t i = 0; i < steps && !e; ++i) e = record_step(c, with_logits, tk);
   hipGraph_t gr = nullptr;
   hipError_t e2 = hipStreamEndCapture(c->stream, &gr);
   if (e) {
@@ -517,6 +523,7 @@ extern "C" frn_status frn_finalize(frn_ctx* c) {
       c->rec_long = lng;
       if ((st = capture(c, true, &c->graph_step[lng], &c->g_step[lng]))) return st;
       if ((st = capture(c, false, &c->graph_prefill[lng], &c->g_prefill[lng]))) return st;
+      if ((st = capture(c, true, &c->graph_multi[lng], &c->g_multi[lng], GREEDY_MULTI))) return st;
     }
     c->rec_long = false;
   }
@@ -694,8 +701,21 @@ extern "C" frn_status frn_decode_greedy(frn_ctx* c, uint32_t id, uint32_t n, con
   bool stopped = false, rolled = false;
   while (done < n && !stopped) {
     const uint32_t b = std::min<uint32_t>(n - done, GREEDY_BATCH), p0 = c->len;
-    for (uint32_t i = 0; i < b; ++i)
+    for (uint32_t i = 0; i < b;) {
+      // GREEDY_MULTI steps in one graph when the token is already on the
+      // device and all of them run the same attention form
+      const bool same_form = (c->len + 1 > ATTENTION_LONG_FROM) == (c->len + GREEDY_MULTI > ATTENTION_LONG_FROM);
+      if (done + i > 0 && b - i >= GREEDY_MULTI && same_form && !c->timing && !(c->cfg.flags & FRN_FLAG_EAGER)) {
+        c->rec_long = c->len + 1 > ATTENTION_LONG_FROM;
+        HIP_TRY(hipGraphLaunch(c->g_multi[c->rec_long], c->stream), "hipGraphLaunch");
+        c->len += GREEDY_MULTI;
+        c->last_next = 0xFFFFFFFFu;
+        i += GREEDY_MULTI;
+        continue;
+      }
       if ((st = run_step(c, id, true, done + i > 0))) return st;
+      ++i;
+    }
     HIP_TRY(hipMemcpyAsync(c->h_hist, c->hist + p0, (size_t)b * 4, hipMemcpyDeviceToHost, c->stream),
             "id read-back");
     HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
