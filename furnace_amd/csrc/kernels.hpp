@@ -93,6 +93,9 @@ __host__ __device__ inline uint32_t attention_split_len(uint32_t T, uint32_t cap
   const uint32_t tiles = (T + ATTENTION_CHUNK - 1) / ATTENTION_CHUNK;
   return ATTENTION_CHUNK * ((tiles + cap - 1) / cap);
 }
+// Query heads of one kv head's group that one attention block handles
+// (the launch's grid z covers the group in blocks of this many).
+uint32_t attention_heads_per_block(uint32_t gq, uint32_t cap);
 // Shapes the attention kernel handles: head_dim 64 or 128, at most 8 query
 // heads per kv head.
 bool attention_supported(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim);
