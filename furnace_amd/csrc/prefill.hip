@@ -11,8 +11,9 @@
 //                     runs v_mfma_f32_32x32x2f32 on them; epilogues: store +
 //                     bias, residual add, SwiGLU of two weights
 //  - k_rope_kv_rows   RoPE of q and k rows at their positions, KV append
-//  - k_attn_rows      causal GQA attention of a block of query rows over
-//                     the cache, online softmax over 64-position key tiles
+//  - k_attn_rows_mfma causal GQA attention of 32 query rows of one head over
+//                     the cache on v_mfma_f32_32x32x2f32 (S^T = K Q^T, then
+//                     O^T += V^T P^T), online softmax over 32-key tiles
 //
 // The MFMA operands are exact f32 (the dequantized weights are exact), so
 // the GEMM differs from the CPU path only by the order of its sums.
@@ -357,77 +358,153 @@ hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const f
   return hipGetLastError();
 }
 
-// ---- causal attention of a block of query rows (model.rs:371-438) ---------------------
-// Block (query head h, 64 query rows): thread t serves query t/4 and dims
-// [HD/4 * (t%4), +HD/4); key tiles of 64 positions from the cache in LDS,
-// online softmax (running max and sum), masked past each query's position.
+// ---- causal attention of a block of query rows on MFMA (model.rs:371-438) ------------
+// Block (32 query rows from q0, query head h), 4 waves; wave w takes the
+// 32-key tiles w, w + 4, ... up to the block's last query position.  With
+// v_mfma_f32_32x32x2f32 (lane l supplies A[l%32][l/32] and B[l/32][l%32];
+// accumulator register v of lane l is C[8(v/4) + 4(l/32) + v%4][l%32]):
+//  - S^T (keys x queries) = K Q^T over the head dims.  Both operands take
+//    the dims in the same permuted order (half l/32 of k-step 4j + c reads
+//    dim 8j + 4(l/32) + c), so each lane loads float4s of its key row and
+//    of its query row.  Lane l then holds the scores of query l%32 for 16
+//    keys; the softmax's running max and sum are 16 in-lane values and one
+//    exchange with lane l^32.
+//  - O^T (dims x queries) += V^T P^T.  The B operand P^T is the S^T
+//    accumulator itself: k-step i takes keys 8(i/4) + 4(l/32) + i%4, the
+//    keys whose scores lane l holds in register i.  A = V^T comes from one
+//    load per lane and k-step, dims DPL*(l%32) .. +DPL of the key's row
+//    (DPL = HD/32); component t feeds M-tile t, whose row m is dim DPL*m + t.
+// The waves' partials (O, m, l) are merged in wave order through LDS.  All
+// products and sums are f32, so only the order of the sums differs from the
+// CPU path (model.rs:371-438).
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_rows(const float* __restrict__ q, const float* __restrict__ kc,
-                                                   const float* __restrict__ vc, float* __restrict__ out, uint32_t nh,
-                                                   uint32_t nkv, uint32_t pos0, uint32_t n, float scale) {
-  constexpr int QT = 64, KT = 64, DS = HD / 4;
-  __shared__ float Ks[KT * (HD + 1)];
-  __shared__ float Vs[KT * HD];
+__global__ __launch_bounds__(256) void k_attn_rows_mfma(const float* __restrict__ q, const float* __restrict__ kc,
+                                                        const float* __restrict__ vc, float* __restrict__ out,
+                                                        uint32_t nh, uint32_t nkv, uint32_t pos0, uint32_t n,
+                                                        float scale) {
+  constexpr int NW = 4, DPL = HD / 32, NQ = HD / 8, OLD = HD + 1;  // O rows padded against bank conflicts
+  __shared__ float mls[NW][2][32];
+  __shared__ float os[32 * OLD];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hh = lane >> 5, col = lane & 31;
   const uint32_t h = blockIdx.y, g = h / (nh / nkv), qd = nh * HD, kvd = nkv * HD;
-  const uint32_t qi = blockIdx.x * QT + threadIdx.x / 4, sub = threadIdx.x % 4;
-  const bool live = qi < n;
-  const uint32_t qpos = pos0 + (live ? qi : 0);
-  float qv[DS], o[DS];
-  const float* qrow = q + (size_t)(live ? qi : 0) * qd + h * HD + sub * DS;
+  const uint32_t q0 = blockIdx.x * 32, qi = q0 + col;
+  const uint32_t qr = qi < n ? qi : n - 1;  // lanes past the block's rows redo row n - 1, not stored
+  const uint32_t qpos = pos0 + qr, last = pos0 + min(n, q0 + 32) - 1;
+  float4 qv[NQ];
+  const float* qrow = q + (size_t)qr * qd + h * HD + 4 * hh;
 #pragma unroll
-  for (int d = 0; d < DS; ++d) {
-    qv[d] = qrow[d];
-    o[d] = 0.f;
+  for (int j = 0; j < NQ; ++j) qv[j] = *(const float4*)(qrow + 8 * j);
+  f32x16 o[DPL];
+#pragma unroll
+  for (int t = 0; t < DPL; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
+  float m = -INFINITY, lsum = 0.f;
+  const float* kbase = kc + (size_t)g * HD + 4 * hh;
+  const float* vbase = vc + (size_t)g * HD + DPL * col;
+  const uint32_t ntiles = last / 32 + 1;
+  for (uint32_t kt = w; kt < ntiles; kt += NW) {
+    // key rows past the last query position are clamped to it (their scores are masked)
+    const float* krow = kbase + (size_t)min(kt * 32 + col, last) * kvd;
+    f32x16 sc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sc[v] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const float4 kv = *(const float4*)(krow + 8 * j);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qv[j].x, sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qv[j].y, sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qv[j].z, sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qv[j].w, sc, 0, 0, 0);
+    }
+    // scale and causal mask (model.rs:384-397), then the online softmax
+    float mx = m;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const uint32_t key = kt * 32 + 8 * (v / 4) + 4 * hh + (v & 3);
+      sc[v] = key <= qpos ? sc[v] * scale : -INFINITY;
+      mx = fmaxf(mx, sc[v]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float ms = mx == -INFINITY ? 0.f : mx;  // no unmasked key yet: keep the exponents finite
+    const float c = expf(m - ms);
+    float ps = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      sc[v] = expf(sc[v] - ms);
+      ps += sc[v];
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    lsum = lsum * c + ps;
+    m = mx;
+#pragma unroll
+    for (int t = 0; t < DPL; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[t][v] *= c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t key = min(kt * 32 + 8 * (i / 4) + 4 * hh + (i & 3), last);
+      const float* vrow = vbase + (size_t)key * kvd;
+      if constexpr (DPL == 4) {
+        const float4 vv = *(const float4*)vrow;
+        o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, sc[i], o[0], 0, 0, 0);
+        o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, sc[i], o[1], 0, 0, 0);
+        o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, sc[i], o[2], 0, 0, 0);
+        o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, sc[i], o[3], 0, 0, 0);
+      } else {
+        const float2 vv = *(const float2*)vrow;
+        o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, sc[i], o[0], 0, 0, 0);
+        o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, sc[i], o[1], 0, 0, 0);
+      }
+    }
   }
-  float m = -INFINITY, l = 0.f;
-  const uint32_t last = pos0 + min(n, blockIdx.x * QT + QT) - 1;  // the tile's last query position
-  for (uint32_t k0 = 0; k0 <= last; k0 += KT) {
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < KT * HD; i += 256) {
-      const uint32_t j = i / HD, d = i % HD, p = k0 + j;
-      const bool ok = p <= last;
-      Ks[j * (HD + 1) + d] = ok ? kc[(size_t)p * kvd + g * HD + d] : 0.f;
-      Vs[j * HD + d] = ok ? vc[(size_t)p * kvd + g * HD + d] : 0.f;
-    }
-    __syncthreads();
-    float sc[KT];
-#pragma unroll
-    for (int j = 0; j < KT; ++j) {
-      float s = 0.f;
-#pragma unroll
-      for (int d = 0; d < DS; ++d) s = fmaf(qv[d], Ks[j * (HD + 1) + sub * DS + d], s);
-      s = group_reduce<4>(s);
-      sc[j] = (k0 + j <= qpos) ? s * scale : -INFINITY;  // model.rs:397, causal mask
-    }
-    float mt = m;
-#pragma unroll
-    for (int j = 0; j < KT; ++j) mt = fmaxf(mt, sc[j]);
-    const float c = expf(m - mt);
-    l *= c;
-#pragma unroll
-    for (int d = 0; d < DS; ++d) o[d] *= c;
-#pragma unroll
-    for (int j = 0; j < KT; ++j) {
-      const float e = expf(sc[j] - mt);
-      l += e;
-#pragma unroll
-      for (int d = 0; d < DS; ++d) o[d] = fmaf(e, Vs[j * HD + sub * DS + d], o[d]);
-    }
-    m = mt;
+  // merge: M = max over the waves, partial w weighted by e^(m_w - M)
+  if (hh == 0) {
+    mls[w][0][col] = m;
+    mls[w][1][col] = lsum;
   }
-  if (!live) return;
-  float* orow = out + (size_t)qi * qd + h * HD + sub * DS;
+  __syncthreads();
+  auto weight = [&](int ww, uint32_t qq, float M) {
+    const float mw = mls[ww][0][qq];
+    return mw == -INFINITY ? 0.f : expf(mw - M);
+  };
+  float M = -INFINITY;
 #pragma unroll
-  for (int d = 0; d < DS; ++d) orow[d] = o[d] / l;
+  for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mls[ww][0][col]);
+  const float e = weight(w, col, M);
+  for (int ww = 0; ww < NW; ++ww) {
+    if (w == ww) {
+#pragma unroll
+      for (int t = 0; t < DPL; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          float* p = os + col * OLD + DPL * (8 * (v / 4) + 4 * hh + (v & 3)) + t;
+          *p = ww == 0 ? e * o[t][v] : *p + e * o[t][v];
+        }
+    }
+    __syncthreads();
+  }
+  // thread t writes query t / 8, dims [HD/8 * (t % 8), +HD/8)
+  const uint32_t qq = threadIdx.x / 8, d0 = (threadIdx.x % 8) * (HD / 8);
+  if (q0 + qq >= n) return;
+  float Mq = -INFINITY, L = 0.f;
+#pragma unroll
+  for (int ww = 0; ww < NW; ++ww) Mq = fmaxf(Mq, mls[ww][0][qq]);
+#pragma unroll
+  for (int ww = 0; ww < NW; ++ww) L += weight(ww, qq, Mq) * mls[ww][1][qq];
+  float* orow = out + (size_t)(q0 + qq) * qd + h * HD + d0;
+#pragma unroll
+  for (int d = 0; d < HD / 8; ++d) orow[d] = os[qq * OLD + d0 + d] / L;
 }
 
 hipError_t launch_attn_rows(const float* q, const float* kc, const float* vc, float* out, uint32_t nh, uint32_t nkv,
                             uint32_t hd, uint32_t pos0, uint32_t n, float scale, hipStream_t s) {
-  dim3 grid((n + 63) / 64, nh);
+  if (n == 0 || nkv == 0 || nh % nkv) return hipErrorInvalidValue;
+  dim3 grid((n + 31) / 32, nh);
   if (hd == 128)
-    hipLaunchKernelGGL((k_attn_rows<128>), grid, dim3(256), 0, s, q, kc, vc, out, nh, nkv, pos0, n, scale);
+    hipLaunchKernelGGL((k_attn_rows_mfma<128>), grid, dim3(256), 0, s, q, kc, vc, out, nh, nkv, pos0, n, scale);
   else if (hd == 64)
-    hipLaunchKernelGGL((k_attn_rows<64>), grid, dim3(256), 0, s, q, kc, vc, out, nh, nkv, pos0, n, scale);
+    hipLaunchKernelGGL((k_attn_rows_mfma<64>), grid, dim3(256), 0, s, q, kc, vc, out, nh, nkv, pos0, n, scale);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
