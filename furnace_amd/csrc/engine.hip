@@ -144,7 +144,13 @@ static hipError_t dmalloc(T** p, size_t bytes) {
 }
 
 // Prefill works on blocks of up to PREFILL_ROWS tokens (64-row GEMM tiles).
-constexpr uint32_t PREFILL_ROWS = 256;
+// Every GEMM's grid grows with the block's rows: at 256 rows the 1.5B
+// hidden-size GEMMs ran 96 blocks on 256 CUs.  Measured (MI355X): 7B
+// 2048-token prompt 5,120 / 6,460 / 7,270 / 8,110 prefill tokens/s at
+// 256 / 512 / 1024 / 2048 rows; 1.5B 4096-token prompt 10,756 / 19,105 /
+// 26,500 / 32,050 / 34,680 at 256 ... 4096.  The scratch is
+// min(max_ctx, 4096) x (3 hidden + 2 kv + ffn) floats: ~500 MB at 7B.
+constexpr uint32_t PREFILL_ROWS = 4096;
 // frn_decode_greedy's steps per host synchronisation (and the most steps
 // that run past a stop id before the host sees it).
 constexpr uint32_t GREEDY_BATCH = 32;

@@ -86,7 +86,7 @@ frn_status frn_finalize(frn_ctx* ctx);
  * (model.rs:579-592, sampler.rs:91-94, generate.rs:69-77): runs the n ids at
  * positions ctx.len .. ctx.len+n, advances ctx.len by n and writes the
  * argmax of the last position's logits (first maximum on ties).  n >= 2
- * runs blocks of up to 256 positions through fp32-MFMA GEMMs on the raw
+ * runs blocks of up to 4096 positions through fp32-MFMA GEMMs on the raw
  * weight blocks (dequantized exactly into LDS tiles). */
 frn_status frn_prefill(frn_ctx* ctx, const uint32_t* ids, uint32_t n, uint32_t* next_id);
 
