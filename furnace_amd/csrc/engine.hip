@@ -155,6 +155,7 @@ constexpr uint32_t PREFILL_ROWS = 4096;
 // that run past a stop id before the host sees it).
 constexpr uint32_t GREEDY_BATCH = 32;
 // decode steps per captured multi-step graph of frn_decode_greedy
+// (8 or 16 steps per graph measured the same: 1,100 tokens/s at 1.5B)
 constexpr uint32_t GREEDY_MULTI = 4;
 
 static hipError_t alloc_prefill(frn_ctx* x) {

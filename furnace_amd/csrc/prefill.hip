@@ -207,35 +207,48 @@ struct Deq8<T_F32> {
   }
 };
 
-// Block tile 64 rows of A (tokens) x 64 weight rows, k-steps of 32; 4 waves,
-// wave (wm, wn) owns the 32x32 output sub-tile (wm, wn) and runs 16
-// v_mfma_f32_32x32x2f32 per k-step.  Lane l supplies A[l%32][l/32] and
-// W[l%32][l/32] of each k-pair; the accumulator's register v of lane l is
-// C[8(v/4) + 4(l/32) + v%4][l%32] (layouts checked on gfx950).
-constexpr int GM = 64, GN = 64, GK = 32, GKP = GK + 1;  // LDS rows padded against bank conflicts
+// Block tile GM = 64 * MT rows of A (tokens) x 64 weight rows, k-steps of
+// 32; 4 waves, wave (wm, wn) owns the 32 * MT x 32 output sub-tile (wm, wn)
+// and runs 16 * MT v_mfma_f32_32x32x2f32 per k-step and weight matrix, so a
+// dequantized weight tile feeds MT times the MFMAs (the single-weight
+// GEMMs are bound by the dequantization at MT 1).  Lane l supplies
+// A[l%32][l/32] and W[l%32][l/32] of each k-pair; the accumulator's
+// register v of lane l is C[8(v/4) + 4(l/32) + v%4][l%32] (layouts checked
+// on gfx950).
+constexpr int GN = 64, GK = 32, GKP = GK + 1;  // LDS rows padded against bank conflicts
 
-template <uint32_t T, int MODE>
+template <uint32_t T, int MODE, int MT>
 __global__ __launch_bounds__(256) void k_gemm_q(GemmArgs g) {
-  constexpr int NW = MODE == GEMM_SWIGLU ? 2 : 1;
+  constexpr int NW = MODE == GEMM_SWIGLU ? 2 : 1, GM = 64 * MT;
   __shared__ float As[GM * GKP];
   __shared__ float Ws[NW][GN * GKP];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave & 1, wn = wave >> 1;
   const uint32_t r0 = blockIdx.y * GM, n0 = blockIdx.x * GN;
-  // tile loaders: thread t fills row t/4, k sub-range 8*(t%4) of A and of W
+  // tile loaders: thread t fills rows t/4 + 64 m (m < MT) of A and row t/4
+  // of W, k sub-range 8*(t%4)
   const uint32_t lr = t / 4, lk = 8 * (t % 4);
   const rsrc_t ra = make_rsrc(g.a, g.P * g.K * 4);
   const rsrc_t rw[2] = {make_rsrc(g.w, g.N * g.row_bytes), make_rsrc(NW == 2 ? g.w2 : g.w, g.N * g.row_bytes)};
-  const bool arow = r0 + lr < g.P, wrow = n0 + lr < g.N;
-  const uint32_t a_off = arow ? 4 * ((r0 + lr) * g.K + lk) : BUF_INVALID;
+  const bool wrow = n0 + lr < g.N;
+  uint32_t a_off[MT];
+  float inv[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const uint32_t r = r0 + lr + 64 * m;
+    a_off[m] = r < g.P ? 4 * (r * g.K + lk) : BUF_INVALID;
+    inv[m] = (g.inv && r < g.P) ? g.inv[r] : 1.0f;
+  }
   const uint32_t w_off = wrow ? (n0 + lr) * g.row_bytes : BUF_INVALID;
-  const float inv = (g.inv && arow) ? g.inv[r0 + lr] : 1.0f;
   const rsrc_t rn = make_rsrc(g.nw, g.nw ? g.K * 4 : 0);
 
-  float4 pa0, pa1, pn0, pn1;
+  float4 pa0[MT], pa1[MT], pn0, pn1;
   Deq8<T> pw[NW];
   auto fetch = [&](uint32_t k0) {
-    pa0 = u4f_(bl128(ra, a_off == BUF_INVALID ? BUF_INVALID : a_off + 4 * k0));
-    pa1 = u4f_(bl128(ra, a_off == BUF_INVALID ? BUF_INVALID : a_off + 4 * k0 + 16));
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      pa0[m] = u4f_(bl128(ra, a_off[m] == BUF_INVALID ? BUF_INVALID : a_off[m] + 4 * k0));
+      pa1[m] = u4f_(bl128(ra, a_off[m] == BUF_INVALID ? BUF_INVALID : a_off[m] + 4 * k0 + 16));
+    }
     if (g.nw) {
       pn0 = u4f_(bl128(rn, 4 * (k0 + lk)));
       pn1 = u4f_(bl128(rn, 4 * (k0 + lk) + 16));
@@ -244,14 +257,17 @@ __global__ __launch_bounds__(256) void k_gemm_q(GemmArgs g) {
     for (int i = 0; i < NW; ++i) pw[i].load(rw[i], w_off, k0 + lk);
   };
   auto stage = [&](uint32_t k0) {
-    float av[8] = {pa0.x, pa0.y, pa0.z, pa0.w, pa1.x, pa1.y, pa1.z, pa1.w};
-    if (g.nw) {  // rmsnorm on load: (x * inv) * w (tensor.rs:181-183)
-      const float nv[8] = {pn0.x, pn0.y, pn0.z, pn0.w, pn1.x, pn1.y, pn1.z, pn1.w};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) av[i] = av[i] * inv * nv[i];
+    for (int m = 0; m < MT; ++m) {
+      float av[8] = {pa0[m].x, pa0[m].y, pa0[m].z, pa0[m].w, pa1[m].x, pa1[m].y, pa1[m].z, pa1[m].w};
+      if (g.nw) {  // rmsnorm on load: (x * inv) * w (tensor.rs:181-183)
+        const float nv[8] = {pn0.x, pn0.y, pn0.z, pn0.w, pn1.x, pn1.y, pn1.z, pn1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) av[i] = av[i] * inv[m] * nv[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) As[(lr + 64 * m) * GKP + lk + i] = av[i];
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) As[lr * GKP + lk + i] = av[i];
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       float y[8];
@@ -261,24 +277,32 @@ __global__ __launch_bounds__(256) void k_gemm_q(GemmArgs g) {
     }
   };
 
-  f32x16 acc[NW];
+  f32x16 acc[MT][NW];
 #pragma unroll
-  for (int w = 0; w < NW; ++w)
+  for (int m = 0; m < MT; ++m)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[w][v] = 0.f;
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[m][w][v] = 0.f;
   const uint32_t nk = g.K / GK;
   fetch(0);
   stage(0);
   __syncthreads();
-  const int ar = wm * 32 + (lane & 31), wr = wn * 32 + (lane & 31), kh = lane >> 5;
+  // wave (wm, wn): A rows wm * 32 * MT + 32 m + lane % 32, W rows wn * 32 + lane % 32
+  const int ar = wm * 32 * MT + (lane & 31), wr = wn * 32 + (lane & 31), kh = lane >> 5;
   for (uint32_t kt = 0; kt < nk; ++kt) {
     if (kt + 1 < nk) fetch((kt + 1) * GK);
 #pragma unroll
     for (int kk = 0; kk < GK; kk += 2) {
-      const float a = As[ar * GKP + kk + kh];
+      float wv[NW];
 #pragma unroll
-      for (int w = 0; w < NW; ++w)
-        acc[w] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, Ws[w][wr * GKP + kk + kh], acc[w], 0, 0, 0);
+      for (int w = 0; w < NW; ++w) wv[w] = Ws[w][wr * GKP + kk + kh];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float a = As[(ar + 32 * m) * GKP + kk + kh];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) acc[m][w] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, wv[w], acc[m][w], 0, 0, 0);
+      }
     }
     __syncthreads();
     if (kt + 1 < nk) {
@@ -291,32 +315,43 @@ __global__ __launch_bounds__(256) void k_gemm_q(GemmArgs g) {
   if (n >= g.N) return;
   const float bias = (MODE == GEMM_STORE && g.bias) ? g.bias[n] : 0.f;
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const uint32_t r = r0 + wm * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v & 3);
-    if (r >= g.P) continue;
-    float* o = g.out + (size_t)r * g.ldo + n;
-    if (MODE == GEMM_STORE) *o = g.bias ? acc[0][v] + bias : acc[0][v];  // model.rs:179-183
-    if (MODE == GEMM_RESID) *o = *o + acc[0][v];                         // tensor.rs:232
-    if (MODE == GEMM_SWIGLU) {                                           // tensor.rs:224
-      const float gg = acc[0][v];
-      *o = gg / (1.0f + expf(-gg)) * acc[NW - 1][v];
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const uint32_t r = r0 + wm * 32 * MT + 32 * m + 8 * (v / 4) + 4 * (lane >> 5) + (v & 3);
+      if (r >= g.P) continue;
+      float* o = g.out + (size_t)r * g.ldo + n;
+      if (MODE == GEMM_STORE) *o = g.bias ? acc[m][0][v] + bias : acc[m][0][v];  // model.rs:179-183
+      if (MODE == GEMM_RESID) *o = *o + acc[m][0][v];                            // tensor.rs:232
+      if (MODE == GEMM_SWIGLU) {                                                 // tensor.rs:224
+        const float gg = acc[m][0][v];
+        *o = gg / (1.0f + expf(-gg)) * acc[m][NW - 1][v];
+      }
     }
+}
+
+// Row blocks of 128 (MT 2) once the prompt block has the rows to keep the
+// grid full; 64 below.  Measured: 7B 2048-token prefill 8,090 -> 8,185
+// tokens/s, 1.5B 4096-token 34,790 -> 35,480 (the GEMMs are not bound by
+// the dequantization alone).
+template <int MODE, int MT>
+static hipError_t gemm_go_mt(const GemmArgs& g, hipStream_t s) {
+  dim3 grid((g.N + GN - 1) / GN, (g.P + 64 * MT - 1) / (64 * MT));
+  switch (g.type) {
+    case T_Q4_K: hipLaunchKernelGGL((k_gemm_q<T_Q4_K, MODE, MT>), grid, dim3(256), 0, s, g); break;
+    case T_Q6_K: hipLaunchKernelGGL((k_gemm_q<T_Q6_K, MODE, MT>), grid, dim3(256), 0, s, g); break;
+    case T_Q8_0: hipLaunchKernelGGL((k_gemm_q<T_Q8_0, MODE, MT>), grid, dim3(256), 0, s, g); break;
+    case T_Q5_0: hipLaunchKernelGGL((k_gemm_q<T_Q5_0, MODE, MT>), grid, dim3(256), 0, s, g); break;
+    case T_F32: hipLaunchKernelGGL((k_gemm_q<T_F32, MODE, MT>), grid, dim3(256), 0, s, g); break;
+    case T_F16: hipLaunchKernelGGL((k_gemm_q<T_F16, MODE, MT>), grid, dim3(256), 0, s, g); break;
+    default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
 }
 
 template <int MODE>
 static hipError_t gemm_go(const GemmArgs& g, hipStream_t s) {
-  dim3 grid((g.N + GN - 1) / GN, (g.P + GM - 1) / GM);
-  switch (g.type) {
-    case T_Q4_K: hipLaunchKernelGGL((k_gemm_q<T_Q4_K, MODE>), grid, dim3(256), 0, s, g); break;
-    case T_Q6_K: hipLaunchKernelGGL((k_gemm_q<T_Q6_K, MODE>), grid, dim3(256), 0, s, g); break;
-    case T_Q8_0: hipLaunchKernelGGL((k_gemm_q<T_Q8_0, MODE>), grid, dim3(256), 0, s, g); break;
-    case T_Q5_0: hipLaunchKernelGGL((k_gemm_q<T_Q5_0, MODE>), grid, dim3(256), 0, s, g); break;
-    case T_F32: hipLaunchKernelGGL((k_gemm_q<T_F32, MODE>), grid, dim3(256), 0, s, g); break;
-    case T_F16: hipLaunchKernelGGL((k_gemm_q<T_F16, MODE>), grid, dim3(256), 0, s, g); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  return g.P >= 512 ? gemm_go_mt<MODE, 2>(g, s) : gemm_go_mt<MODE, 1>(g, s);
 }
 
 hipError_t launch_gemm(const GemmArgs& g, GemmMode mode, hipStream_t s) {
