@@ -839,13 +839,15 @@ hipError_t launch_embed(const uint8_t* table, uint32_t type, uint32_t hidden, ui
 //    kernel copied from the host-computed table, made with the CPU path's
 //    powf/sinf/cosf; the rotation is evaluated without FMA contraction, so
 //    q/k match the CPU bit for bit given equal inputs);
-//  - the block holding the step position appends head g's k/v to the cache;
+//  - the z = 0 block holding the step position appends head g's k/v to the
+//    cache;
 //  - per sub-tile: scores from K rows in registers, softmax with the
 //    running max and sum of the split, P.V from V rows in LDS; the next
 //    sub-tile's rows are loaded while this one's softmax and P.V run;
 //  - writes its partial (o = sum_t e^(s_t - m) v_t, m, l = sum_t e^(s_t - m))
 //    per query head to `part`; the o-proj GEMV (GEMV_RESID_ATT) merges the
-//    splits while it stages its input, so no block waits on another here.
+//    splits while it stages its input (k_attn_merge in the long-context
+//    form), so no block waits on another here.
 template <int HD, int GQ>
 __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, const float* __restrict__ kn,
                                                    const float* __restrict__ vn, const float* __restrict__ cs,
