@@ -64,8 +64,10 @@ typedef struct frn_ctx frn_ctx;
 
 /* Allocate a context on HIP device `device`: the KV cache (f32,
  * [n_layers][max_ctx][n_kv_heads*head_dim] for K and V, model.rs:321-339),
- * activation buffers and the RoPE table.  Replaces Model::load's allocation
- * side (model.rs:520-552) and KvCache::new (model.rs:330-339). */
+ * activation buffers, the RoPE table and the prefill's row buffers
+ * (min(max_ctx, 4096) rows of 3*hidden + 2*kv_dim + ffn floats: ~500 MB at
+ * Qwen2-7B shape).  Replaces Model::load's allocation side
+ * (model.rs:520-552) and KvCache::new (model.rs:330-339). */
 frn_status frn_create(const frn_config* cfg, int device, frn_ctx** out);
 
 /* Copy one GGUF tensor from host memory (e.g. the mmap) to HBM, raw.
