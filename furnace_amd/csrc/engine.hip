@@ -94,6 +94,8 @@ struct frn_ctx {
   bool sampler_ready = false;
   float s_temperature = 0.f, s_top_p = 1.f, s_penalty = 1.f;
   uint32_t s_top_k = 0;
+  bool s_full = false;  // top_k 0 or above SAMPLER_MAX_K: the whole-vocabulary path
+  SamplerFull full;     // its buffers, allocated by the first frn_sampler_init that needs them
   // prefill rows: blocks of up to pf_rows prompt tokens through all layers
   uint32_t pf_rows = 0;
   float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_att = nullptr, *pf_act = nullptr,
@@ -127,7 +129,7 @@ static void free_ctx(frn_ctx* c) {
   }
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.keys_sorted, c->full.ids, c->full.ids_sorted, c->full.tmp, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -786,13 +788,27 @@ extern "C" frn_status frn_sampler_init(frn_ctx* c, float temperature, uint32_t t
   if (!(repeat_penalty > 0.0f) || !std::isfinite(repeat_penalty))
     return fail(FRN_EINVAL, "frn_sampler_init: repeat_penalty %g must be finite and > 0", (double)repeat_penalty);
   const bool draw = !(temperature == 0.0f || top_k == 1);
-  if (draw && (top_k == 0 || top_k > SAMPLER_MAX_K))
-    return fail(FRN_EINVAL, "frn_sampler_init: the device sampler takes top_k 1..%u (got %u; 0 = no cut is not supported)",
-                SAMPLER_MAX_K, top_k);
-  if (sampler_sort_size(c->cfg.vocab, draw ? top_k : 1) > SAMPLER_MAX_SORT)
+  // top_k 0 (no cut) and top_k above SAMPLER_MAX_K sort the whole vocabulary
+  const bool full = draw && (top_k == 0 || top_k > SAMPLER_MAX_K);
+  if (!full && sampler_sort_size(c->cfg.vocab, draw ? top_k : 1) > SAMPLER_MAX_SORT)
     return fail(FRN_EINVAL, "frn_sampler_init: vocab %u x top_k %u candidates exceed the %u the sampler sorts",
                 c->cfg.vocab, top_k, SAMPLER_MAX_SORT);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  if (full && !c->full.keys) {
+    const size_t V = c->cfg.vocab;
+    SamplerFull f;
+    hipError_t e;
+    if ((e = sampler_full_tmp_bytes(c->cfg.vocab, &f.tmp_bytes)) || (e = dmalloc(&f.keys, V * 4)) ||
+        (e = dmalloc(&f.keys_sorted, V * 4)) || (e = dmalloc(&f.ids, V * 4)) || (e = dmalloc(&f.ids_sorted, V * 4)) ||
+        (e = dmalloc(&f.tmp, f.tmp_bytes ? f.tmp_bytes : 1))) {
+      void* ps[] = {f.keys, f.keys_sorted, f.ids, f.ids_sorted, f.tmp};
+      for (void* q : ps)
+        if (q) (void)hipFree(q);
+      return fail(e == hipErrorOutOfMemory ? FRN_EOOM : FRN_EHIP, "frn_sampler_init: whole-vocabulary buffers: %s",
+                  hipGetErrorString(e));
+    }
+    c->full = f;
+  }
   HIP_TRY(sampler_prepare(c->cfg.vocab, SAMPLER_MAX_K), "sampler LDS limit");
   SamplerRng r{0, (0xda3e39cb94b95bdbull << 1) | 1u, 0};
   pcg32_step(r);
@@ -803,6 +819,7 @@ extern "C" frn_status frn_sampler_init(frn_ctx* c, float temperature, uint32_t t
   HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
   c->s_temperature = temperature;
   c->s_top_k = top_k;
+  c->s_full = full;
   c->s_top_p = top_p;
   c->s_penalty = repeat_penalty;
   c->sampler_ready = true;
@@ -828,10 +845,15 @@ extern "C" frn_status frn_sample(frn_ctx* c, const uint32_t* recent, uint32_t n_
     HIP_TRY(hipMemcpyAsync(c->recent, c->h_recent, (size_t)n_recent * 4, hipMemcpyHostToDevice, c->stream),
             "recent ids upload");
   }
-  HIP_TRY(launch_sample(c->logits, c->cfg.vocab, c->recent, n_recent, c->s_penalty,
-                        draw ? c->s_temperature : 1.0f, draw ? std::min(c->s_top_k, SAMPLER_MAX_K) : 1u,
-                        c->s_top_p, draw, c->cand_v, c->cand_id, c->rng, c->st, c->stream),
-          "sampler launch");
+  if (draw && c->s_full)
+    HIP_TRY(launch_sample_full(c->logits, c->cfg.vocab, c->recent, n_recent, c->s_penalty, c->s_temperature,
+                               c->s_top_k, c->s_top_p, c->full, c->rng, c->st, c->stream),
+            "sampler launch (whole vocabulary)");
+  else
+    HIP_TRY(launch_sample(c->logits, c->cfg.vocab, c->recent, n_recent, c->s_penalty,
+                          draw ? c->s_temperature : 1.0f, draw ? std::min(c->s_top_k, SAMPLER_MAX_K) : 1u,
+                          c->s_top_p, draw, c->cand_v, c->cand_id, c->rng, c->st, c->stream),
+            "sampler launch");
   frn_status st = read_next(c, next_id);
   // the host buffer is reused by the next call: the copy above has run
   return st;

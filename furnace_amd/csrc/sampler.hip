@@ -12,6 +12,14 @@
 //    top-p cumulative sum, renormalization, cumulative draw), with the
 //    PCG32 state in device memory.
 //
+// top_k 0 ("no cut") and top_k above 64 take the whole-vocabulary path:
+//  k_sample_full_keys: the penalty and temperature per logit;
+//  a stable radix sort of all (value, id) pairs by descending value
+//    (hipCUB), so equal values keep ascending ids as above;
+//  k_sample_full_pick: the softmax terms in parallel, then one thread runs
+//    the same sequential sums over the sorted vocabulary while the block
+//    stages each next stretch of terms (or probabilities) through LDS.
+//
 // Ties among equal scaled logits are taken in ascending id order; the
 // reference's select_nth_unstable_by / sort_unstable_by leave their order
 // unspecified.  exp is evaluated in f64 and rounded to f32, which agrees with
@@ -20,6 +28,8 @@
 #include "sampler.hpp"
 
 #include <math.h>
+
+#include <hipcub/hipcub.hpp>
 
 namespace frn {
 
@@ -156,9 +166,148 @@ __global__ __launch_bounds__(1024) void k_sample_pick(const float* __restrict__ 
   st->tok = pick;
 }
 
+// the penalty and temperature of every logit (as k_sample_cand), ids in order
+__global__ __launch_bounds__(256) void k_sample_full_keys(const float* __restrict__ logits, uint32_t vocab,
+                                                          const uint32_t* __restrict__ recent, uint32_t n_recent,
+                                                          float penalty, float temperature, float* __restrict__ keys,
+                                                          uint32_t* __restrict__ ids) {
+  __shared__ uint32_t rec[SAMPLER_MAX_RECENT];
+  for (uint32_t i = threadIdx.x; i < n_recent; i += blockDim.x) rec[i] = recent[i];
+  __syncthreads();
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= vocab) return;
+  float x = logits[t];
+  if (penalty != 1.0f) {  // apply_repeat_penalty (sampler.rs:39-55)
+    bool hit = false;
+    for (uint32_t r = 0; r < n_recent; ++r) hit |= rec[r] == t;
+    if (hit) x = x > 0.0f ? x / penalty : x * penalty;
+  }
+  x = x / temperature;  // filtered(), sampler.rs:121-125
+  if (x == 0.0f) x = 0.0f;  // -0 sorts with +0: the reference compares them equal
+  keys[t] = x;
+  ids[t] = t;
+}
+
+// Sequential passes over the sorted candidates (Sampler::filtered and the
+// draw, sampler.rs:97-154) by thread 0, in the reference's order; the block
+// stages FULL_CHUNK values at a time through LDS, computing each pass's
+// per-element values (terms, terms / sum, their renormalization) in
+// parallel with the same single divisions.
+constexpr uint32_t FULL_CHUNK = 8192;
+__global__ __launch_bounds__(1024) void k_sample_full_pick(const float* __restrict__ v, float* __restrict__ e,
+                                                           const uint32_t* __restrict__ id, uint32_t vocab,
+                                                           uint32_t k, float top_p, SamplerRng* rng,
+                                                           StepState* st) {
+  __shared__ float buf[FULL_CHUNK];
+  __shared__ float sh_val;
+  __shared__ uint32_t sh_idx, sh_done;
+  const uint32_t len0 = (k > 0 && k < vocab) ? k : vocab;  // top-k cut, else every candidate
+  // softmax terms e^(v_i - max), max = v_0 (sampler.rs:131-137); e is a
+  // buffer this kernel has not read, so its reads see these writes
+  const float mx = v[0];
+  for (uint32_t i = threadIdx.x; i < len0; i += blockDim.x) e[i] = (float)exp((double)(v[i] - mx));
+  __syncthreads();
+  // pass: stage f(i) for i < len in chunks; thread 0 folds them in order
+  // until it sets sh_done.  f and fold see the chunk's base index.
+  auto pass = [&](uint32_t len, auto&& f, auto&& fold) {
+    if (threadIdx.x == 0) sh_done = 0;
+    __syncthreads();
+    for (uint32_t c0 = 0; c0 < len; c0 += FULL_CHUNK) {
+      const uint32_t n = min(FULL_CHUNK, len - c0);
+      for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) buf[i] = f(c0 + i);
+      __syncthreads();
+      if (threadIdx.x == 0) fold(c0, n);
+      __syncthreads();
+      if (sh_done) break;
+    }
+  };
+  float sum = 0.0f;  // thread 0's running values
+  pass(len0, [&](uint32_t i) { return e[i]; }, [&](uint32_t, uint32_t n) {
+    for (uint32_t i = 0; i < n; ++i) sum += buf[i];
+  });
+  if (threadIdx.x == 0) sh_val = sum;
+  __syncthreads();
+  sum = sh_val;
+  uint32_t len = len0;
+  float t = 1.0f;
+  if (top_p < 1.0f) {  // keep through the crossing token, then renormalize (sampler.rs:143-153)
+    float cum = 0.0f;
+    if (threadIdx.x == 0) sh_idx = len0;
+    pass(len0, [&](uint32_t i) { return e[i] / sum; }, [&](uint32_t c0, uint32_t n) {
+      for (uint32_t i = 0; i < n; ++i) {
+        cum += buf[i];
+        if (cum >= top_p) {
+          sh_idx = c0 + i + 1;
+          sh_done = 1;
+          break;
+        }
+      }
+    });
+    __syncthreads();
+    len = sh_idx;
+    float s2 = 0.0f;
+    pass(len, [&](uint32_t i) { return e[i] / sum; }, [&](uint32_t, uint32_t n) {
+      for (uint32_t i = 0; i < n; ++i) s2 += buf[i];
+    });
+    if (threadIdx.x == 0) sh_val = s2;
+    __syncthreads();
+    t = sh_val;
+  }
+  // the draw (sampler.rs:97-107): u in [0, 1) from the top 24 bits
+  float u = 0.0f;
+  if (threadIdx.x == 0) {
+    SamplerRng r = *rng;
+    u = (float)(pcg32_next(&r) >> 8) / (float)(1u << 24);
+    r.draws += 1;
+    *rng = r;
+    sh_idx = len - 1;  // candidates.last() when the cumulative sum never passes u
+  }
+  float cum = 0.0f;
+  const bool renorm = top_p < 1.0f;
+  pass(len, [&](uint32_t i) { const float p = e[i] / sum; return renorm ? p / t : p; },
+       [&](uint32_t c0, uint32_t n) {
+         for (uint32_t i = 0; i < n; ++i) {
+           cum += buf[i];
+           if (u < cum) {
+             sh_idx = c0 + i;
+             sh_done = 1;
+             break;
+           }
+         }
+       });
+  if (threadIdx.x == 0) {
+    const uint32_t pick = id[sh_idx];
+    st->next_tok = pick;
+    st->tok = pick;
+  }
+}
+
 }  // namespace
 
 uint32_t sampler_blocks(uint32_t vocab) { return (vocab + CAND_BLOCK - 1) / CAND_BLOCK; }
+
+hipError_t sampler_full_tmp_bytes(uint32_t vocab, size_t* bytes) {
+  *bytes = 0;
+  return hipcub::DeviceRadixSort::SortPairsDescending(nullptr, *bytes, (const float*)nullptr, (float*)nullptr,
+                                                      (const uint32_t*)nullptr, (uint32_t*)nullptr, (int)vocab);
+}
+
+hipError_t launch_sample_full(const float* logits, uint32_t vocab, const uint32_t* recent, uint32_t n_recent,
+                              float penalty, float temperature, uint32_t k, float top_p, const SamplerFull& f,
+                              SamplerRng* rng, StepState* st, hipStream_t s) {
+  if (n_recent > SAMPLER_MAX_RECENT || !f.keys || !f.tmp || vocab == 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_sample_full_keys, dim3((vocab + 255) / 256), dim3(256), 0, s, logits, vocab, recent, n_recent,
+                     penalty, temperature, f.keys, f.ids);
+  hipError_t e = hipGetLastError();
+  if (e) return e;
+  size_t bytes = f.tmp_bytes;
+  if ((e = hipcub::DeviceRadixSort::SortPairsDescending(f.tmp, bytes, f.keys, f.keys_sorted, f.ids, f.ids_sorted,
+                                                        (int)vocab, 0, 32, s)))
+    return e;
+  hipLaunchKernelGGL(k_sample_full_pick, dim3(1), dim3(1024), 0, s, f.keys_sorted, f.keys, f.ids_sorted, vocab, k,
+                     top_p, rng, st);
+  return hipGetLastError();
+}
 
 uint32_t sampler_sort_size(uint32_t vocab, uint32_t k) {
   uint32_t n = sampler_blocks(vocab) * k, n2 = 1;

@@ -28,4 +28,21 @@ hipError_t launch_sample(const float* logits, uint32_t vocab, const uint32_t* re
                          float penalty, float temperature, uint32_t k, float top_p, bool draw, float* cand_v,
                          uint32_t* cand_id, SamplerRng* rng, StepState* st, hipStream_t s);
 
+// The whole-vocabulary path, for top_k 0 ("no cut") and top_k above
+// SAMPLER_MAX_K: every candidate sorted, then the reference's sequential
+// softmax sum, top-p cumulative sum, renormalization and draw.  Buffers of
+// `vocab` entries and the radix sort's temporary storage.
+struct SamplerFull {
+  float* keys = nullptr;         // scaled logits, then the softmax terms
+  float* keys_sorted = nullptr;  // scaled logits in descending order
+  uint32_t* ids = nullptr;
+  uint32_t* ids_sorted = nullptr;
+  void* tmp = nullptr;
+  size_t tmp_bytes = 0;
+};
+hipError_t sampler_full_tmp_bytes(uint32_t vocab, size_t* bytes);
+hipError_t launch_sample_full(const float* logits, uint32_t vocab, const uint32_t* recent, uint32_t n_recent,
+                              float penalty, float temperature, uint32_t k, float top_p, const SamplerFull& f,
+                              SamplerRng* rng, StepState* st, hipStream_t s);
+
 }  // namespace frn

@@ -112,9 +112,10 @@ frn_status frn_decode_greedy(frn_ctx* ctx, uint32_t id, uint32_t n, const uint32
 /* Sampler::new (sampler.rs:68-78) on the device: temperature, top_k, top_p,
  * repeat penalty (1.0 disables) and the PCG32 seed (Pcg32::new).  At
  * temperature 0 or top_k 1, frn_sample is the argmax of the penalized logits
- * and takes no RNG draw (sampler.rs:91-94).  Otherwise top_k must be 1..64:
- * the reference's top_k 0 ("no cut") is not supported on the device and is
- * rejected (FRN_EINVAL). */
+ * and takes no RNG draw (sampler.rs:91-94).  top_k 2..64 keeps per-block
+ * candidates; top_k 0 ("no cut") and top_k above 64 sort the whole
+ * vocabulary on the device (the first such call allocates 4 buffers of
+ * vocab entries and the sort's temporary storage). */
 frn_status frn_sampler_init(frn_ctx* ctx, float temperature, uint32_t top_k, float top_p, float repeat_penalty,
                             uint64_t seed);
 

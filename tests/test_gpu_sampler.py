@@ -24,6 +24,10 @@ CASES = [  # temperature, top_k, top_p, repeat_penalty, n_recent
     (0.05, 17, 0.95, 0.8, 10),
     (0.0, 40, 0.9, 1.5, 64),   # temperature 0: argmax of the penalized logits, no draw
     (0.8, 1, 0.9, 1.2, 64),    # top_k 1: the same
+    # the whole-vocabulary path: every candidate sorted, then the sequential sums
+    (0.7, 0, 0.9, 1.0, 0),     # top_k 0 (no cut) with the default top_p
+    (1.0, 0, 1.0, 1.1, 20),    # no cut at all: the draw walks the sorted vocabulary
+    (0.8, 100, 0.95, 1.0, 0),  # top_k above the 64 the candidate path keeps
 ]
 
 
@@ -83,11 +87,11 @@ def test_sampled_generation_loop(hip, tmpdir_models):
 def test_sampler_rejects_unsupported_settings(hip, tmpdir_models):
     m = _model(tmpdir_models)
     with pytest.raises(fa.FrnError):
-        m.sampler_init(0.7, 0, 0.9)   # top_k 0 (no cut) is not supported on the device
-    with pytest.raises(fa.FrnError):
-        m.sampler_init(0.7, 65, 0.9)
-    with pytest.raises(fa.FrnError):
         m.sampler_init(-1.0, 40, 0.9)
+    with pytest.raises(fa.FrnError):
+        m.sampler_init(0.7, 40, float("nan"))
+    with pytest.raises(fa.FrnError):
+        m.sampler_init(0.7, 40, 0.9, 0.0)  # repeat penalty must be > 0
     m.sampler_init(0.7, 40, 0.9)
     with pytest.raises(fa.FrnError):
         m.sample()                    # no logits yet
