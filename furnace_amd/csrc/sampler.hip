@@ -189,16 +189,22 @@ __global__ __launch_bounds__(256) void k_sample_full_keys(const float* __restric
 }
 
 // Sequential passes over the sorted candidates (Sampler::filtered and the
-// draw, sampler.rs:97-154) by thread 0, in the reference's order; the block
-// stages FULL_CHUNK values at a time through LDS, computing each pass's
+// draw, sampler.rs:97-154) in the reference's order.  The block stages
+// FULL_CHUNK values at a time through LDS, computing each pass's
 // per-element values (terms, terms / sum, their renormalization) in
-// parallel with the same single divisions.
+// parallel with the same single divisions; thread 0 then folds them in
+// order, 16 at a time: four float4 LDS reads (the next group's issued
+// before this group is added), 16 dependent f32 adds, and for the passes
+// that stop at a crossing one test per group on the last running sum (the
+// sums only grow, so the first crossing lies in the first group whose last
+// sum crosses).
 constexpr uint32_t FULL_CHUNK = 8192;
+constexpr int FOLD = 16;
 __global__ __launch_bounds__(1024) void k_sample_full_pick(const float* __restrict__ v, float* __restrict__ e,
                                                            const uint32_t* __restrict__ id, uint32_t vocab,
                                                            uint32_t k, float top_p, SamplerRng* rng,
                                                            StepState* st) {
-  __shared__ float buf[FULL_CHUNK];
+  __shared__ __align__(16) float buf[FULL_CHUNK];
   __shared__ float sh_val;
   __shared__ uint32_t sh_idx, sh_done;
   const uint32_t len0 = (k > 0 && k < vocab) ? k : vocab;  // top-k cut, else every candidate
@@ -207,24 +213,69 @@ __global__ __launch_bounds__(1024) void k_sample_full_pick(const float* __restri
   const float mx = v[0];
   for (uint32_t i = threadIdx.x; i < len0; i += blockDim.x) e[i] = (float)exp((double)(v[i] - mx));
   __syncthreads();
-  // pass: stage f(i) for i < len in chunks; thread 0 folds them in order
-  // until it sets sh_done.  f and fold see the chunk's base index.
-  auto pass = [&](uint32_t len, auto&& f, auto&& fold) {
-    if (threadIdx.x == 0) sh_done = 0;
+  // pass: stage f(i) for i < len in chunks; thread 0 runs acc += x over
+  // them in order.  With `stop`, the pass ends at the first i where
+  // crossed(acc) holds and returns that i, else len.
+  auto pass = [&](uint32_t len, float& acc, bool stop, auto&& f, auto&& crossed) -> uint32_t {
+    if (threadIdx.x == 0) {
+      sh_done = 0;
+      sh_idx = len;
+    }
     __syncthreads();
     for (uint32_t c0 = 0; c0 < len; c0 += FULL_CHUNK) {
       const uint32_t n = min(FULL_CHUNK, len - c0);
       for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) buf[i] = f(c0 + i);
       __syncthreads();
-      if (threadIdx.x == 0) fold(c0, n);
+      if (threadIdx.x == 0) {
+        const float4* b4 = (const float4*)buf;
+        const uint32_t ng = n / FOLD;
+        float4 q[FOLD / 4];
+#pragma unroll
+        for (int w = 0; w < FOLD / 4; ++w) q[w] = b4[w];  // group 0 (inside buf even when ng == 0)
+        for (uint32_t g = 0; g < ng; ++g) {
+          float x[FOLD];
+#pragma unroll
+          for (int w = 0; w < FOLD / 4; ++w) {
+            x[4 * w] = q[w].x;
+            x[4 * w + 1] = q[w].y;
+            x[4 * w + 2] = q[w].z;
+            x[4 * w + 3] = q[w].w;
+          }
+          if (g + 1 < ng)
+#pragma unroll
+            for (int w = 0; w < FOLD / 4; ++w) q[w] = b4[(g + 1) * (FOLD / 4) + w];
+          float run[FOLD];
+#pragma unroll
+          for (int j = 0; j < FOLD; ++j) {
+            acc += x[j];
+            run[j] = acc;
+          }
+          if (stop && crossed(run[FOLD - 1])) {
+            int j = 0;
+            while (!crossed(run[j])) ++j;
+            sh_idx = c0 + g * FOLD + j;
+            sh_done = 1;
+            break;
+          }
+        }
+        if (!sh_done)
+          for (uint32_t i = ng * FOLD; i < n; ++i) {  // the chunk's tail
+            acc += buf[i];
+            if (stop && crossed(acc)) {
+              sh_idx = c0 + i;
+              sh_done = 1;
+              break;
+            }
+          }
+      }
       __syncthreads();
       if (sh_done) break;
     }
+    return sh_idx;
   };
+  auto never = [](float) { return false; };
   float sum = 0.0f;  // thread 0's running values
-  pass(len0, [&](uint32_t i) { return e[i]; }, [&](uint32_t, uint32_t n) {
-    for (uint32_t i = 0; i < n; ++i) sum += buf[i];
-  });
+  pass(len0, sum, false, [&](uint32_t i) { return e[i]; }, never);
   if (threadIdx.x == 0) sh_val = sum;
   __syncthreads();
   sum = sh_val;
@@ -232,23 +283,12 @@ __global__ __launch_bounds__(1024) void k_sample_full_pick(const float* __restri
   float t = 1.0f;
   if (top_p < 1.0f) {  // keep through the crossing token, then renormalize (sampler.rs:143-153)
     float cum = 0.0f;
-    if (threadIdx.x == 0) sh_idx = len0;
-    pass(len0, [&](uint32_t i) { return e[i] / sum; }, [&](uint32_t c0, uint32_t n) {
-      for (uint32_t i = 0; i < n; ++i) {
-        cum += buf[i];
-        if (cum >= top_p) {
-          sh_idx = c0 + i + 1;
-          sh_done = 1;
-          break;
-        }
-      }
-    });
+    const uint32_t at = pass(len0, cum, true, [&](uint32_t i) { return e[i] / sum; },
+                             [&](float c) { return c >= top_p; });
     __syncthreads();
-    len = sh_idx;
+    len = at < len0 ? at + 1 : len0;
     float s2 = 0.0f;
-    pass(len, [&](uint32_t i) { return e[i] / sum; }, [&](uint32_t, uint32_t n) {
-      for (uint32_t i = 0; i < n; ++i) s2 += buf[i];
-    });
+    pass(len, s2, false, [&](uint32_t i) { return e[i] / sum; }, never);
     if (threadIdx.x == 0) sh_val = s2;
     __syncthreads();
     t = sh_val;
@@ -260,23 +300,13 @@ __global__ __launch_bounds__(1024) void k_sample_full_pick(const float* __restri
     u = (float)(pcg32_next(&r) >> 8) / (float)(1u << 24);
     r.draws += 1;
     *rng = r;
-    sh_idx = len - 1;  // candidates.last() when the cumulative sum never passes u
   }
   float cum = 0.0f;
   const bool renorm = top_p < 1.0f;
-  pass(len, [&](uint32_t i) { const float p = e[i] / sum; return renorm ? p / t : p; },
-       [&](uint32_t c0, uint32_t n) {
-         for (uint32_t i = 0; i < n; ++i) {
-           cum += buf[i];
-           if (u < cum) {
-             sh_idx = c0 + i;
-             sh_done = 1;
-             break;
-           }
-         }
-       });
+  const uint32_t at = pass(len, cum, true, [&](uint32_t i) { const float p = e[i] / sum; return renorm ? p / t : p; },
+                           [&](float c) { return u < c; });
   if (threadIdx.x == 0) {
-    const uint32_t pick = id[sh_idx];
+    const uint32_t pick = id[at < len ? at : len - 1];  // candidates.last() when the sum never passes u
     st->next_tok = pick;
     st->tok = pick;
   }
