@@ -101,16 +101,17 @@ def test_sampler_rejects_unsupported_settings(hip, tmpdir_models):
     m.close()
 
 
-def test_generate_sampled_is_the_sampling_loop(hip, tmpdir_models):
+@pytest.mark.parametrize("top_k", [40, 0])
+def test_generate_sampled_is_the_sampling_loop(hip, tmpdir_models, top_k):
     # frn_generate_sampled (the host layer's generate.rs loop) against the
     # same loop driven step by step: prefill, sample over the last 64 ids,
-    # stop check, decode
+    # stop check, decode (top_k 0: the whole-vocabulary path)
     m = _model(tmpdir_models)
     prompt = list(np.random.default_rng(8).integers(0, SPEC["vocab"], 12).astype(np.uint32))
-    ids, st, draws = m.generate_sampled(prompt, 30, 0.8, 40, 0.9, 1.1, seed=5, stop_ids=[])
+    ids, st, draws = m.generate_sampled(prompt, 30, 0.8, top_k, 0.9, 1.1, seed=5, stop_ids=[])
     assert len(ids) == 30 and st.decode_steps == 29 and draws == 30
     m.reset()
-    m.sampler_init(0.8, 40, 0.9, 1.1, seed=5)
+    m.sampler_init(0.8, top_k, 0.9, 1.1, seed=5)
     m.prefill(np.array(prompt, np.uint32))
     context, loop = list(prompt), []
     for step in range(30):
