@@ -20,6 +20,8 @@ BLOCK = {F32: (1, 4), F16: (1, 2), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 1
 
 FLAG_EAGER = 1  # FRN_FLAG_EAGER
 FLAG_STEPWISE_PREFILL = 2  # FRN_FLAG_STEPWISE_PREFILL
+FLAG_NO_RESIDENT = 4  # FRN_FLAG_NO_RESIDENT
+FLAG_RESIDENT = 8  # FRN_FLAG_RESIDENT
 
 MIX_ALL_Q8_0, MIX_Q4_K_M, MIX_ALL_Q4_K, MIX_ALL_Q6_K, MIX_ALL_Q5_0, MIX_ALL_F32, MIX_Q4_K_M_LLAMA, MIX_ALL_F16 = range(8)
 
@@ -68,6 +70,8 @@ SIGNATURES = {
     "frn_prefill": (_I, [_P, _P, _U32, ctypes.POINTER(_U32)]),
     "frn_decode": (_I, [_P, _U32, ctypes.POINTER(_U32)]),
     "frn_decode_greedy": (_I, [_P, _U32, _U32, _P, _U32, _P, ctypes.POINTER(_U32)]),
+    "frn_decode_engine": (_I, [_P, ctypes.POINTER(_U32), ctypes.c_char_p, _SZ]),
+    "frn_resident_trace": (_I, [_P, _U32, _P, _SZ]),
     "frn_sampler_init": (_I, [_P, ctypes.c_float, _U32, ctypes.c_float, ctypes.c_float, ctypes.c_uint64]),
     "frn_sample": (_I, [_P, _P, _U32, ctypes.POINTER(_U32)]),
     "frn_sampler_draws": (_I, [_P, ctypes.POINTER(ctypes.c_uint64)]),
@@ -250,7 +254,7 @@ def synth_write(path, seed, threads=0, weight_std=0.02, rope_theta=1e6, rms_eps=
 class Model:
     """A GGUF model loaded onto one GPU: Model::load + KvCache in one context."""
 
-    def __init__(self, path, device=0, max_ctx=4096, eager=False, stepwise_prefill=False):
+    def __init__(self, path, device=0, max_ctx=4096, eager=False, stepwise_prefill=False, resident=None):
         lib = load()
         self.gguf = ctypes.c_void_p()
         check(lib.frn_gguf_open(path.encode(), ctypes.byref(self.gguf)))
@@ -259,7 +263,8 @@ class Model:
         check(lib.frn_gguf_config(self.gguf, ctypes.byref(self.cfg), ctypes.byref(ctx_len)))
         self.context_length = ctx_len.value
         self.ctx = ctypes.c_void_p()
-        flags = (FLAG_EAGER if eager else 0) | (FLAG_STEPWISE_PREFILL if stepwise_prefill else 0)
+        flags = ((FLAG_EAGER if eager else 0) | (FLAG_STEPWISE_PREFILL if stepwise_prefill else 0) |
+                 (0 if resident is None else FLAG_RESIDENT if resident else FLAG_NO_RESIDENT))
         check(lib.frn_model_load(self.gguf, device, max_ctx, flags, ctypes.byref(self.ctx)))
         self.cfg.max_ctx = max_ctx
         self.vocab = self.cfg.vocab
@@ -283,6 +288,25 @@ class Model:
         nxt = ctypes.c_uint32()
         check(load().frn_decode(self.ctx, int(tok), ctypes.byref(nxt)))
         return nxt.value
+
+    def decode_engine(self):
+        """(resident, reason): 1 when the resident decode kernel serves
+        decode steps, else 0 and why not (frn_decode_engine)."""
+        on = ctypes.c_uint32()
+        why = ctypes.create_string_buffer(256)
+        check(load().frn_decode_engine(self.ctx, ctypes.byref(on), why, 256))
+        return on.value, why.value.decode()
+
+    def resident_trace(self, n_steps, read=False):
+        """Arm (read=False) or read (read=True) the resident kernel's phase
+        timestamps: [n_steps][n_layers + 1][16][256] uint64 at 100 MHz."""
+        if not read:
+            check(load().frn_resident_trace(self.ctx, n_steps, None, 0))
+            return None
+        shape = (n_steps, self.cfg.n_layers + 1, 16, 256)
+        out = np.zeros(shape, dtype=np.uint64)
+        check(load().frn_resident_trace(self.ctx, n_steps, out.ctypes.data, out.size))
+        return out
 
     def decode_greedy(self, tok, n, stop_ids=()):
         """n greedy steps from token tok (frn_decode_greedy): the ids of the

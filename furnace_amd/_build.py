@@ -24,7 +24,7 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
              "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__"]
 
-HIP_SOURCES = ["kernels.hip", "prefill.hip", "sampler.hip", "engine.hip"]
+HIP_SOURCES = ["kernels.hip", "prefill.hip", "sampler.hip", "resident.hip", "engine.hip"]
 HOST_SOURCES = ["host/errors.cpp", "host/gguf.cpp", "host/model.cpp", "host/synth.cpp"]
 
 

@@ -9,6 +9,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -21,6 +22,7 @@
 #include "common.hpp"
 #include "formats.hpp"
 #include "kernels.hpp"
+#include "resident.hpp"
 #include "sampler.hpp"
 
 using namespace frn;
@@ -115,6 +117,21 @@ struct frn_ctx {
   std::vector<int> ev_cat;
   double t_ms[N_CAT] = {0};
   uint64_t t_calls[N_CAT] = {0};
+  // resident decode (resident.hip): the whole greedy loop in one launch
+  bool res_ok = false;
+  std::string res_why = "not finalized";
+  ResArgs* h_res = nullptr;   // pinned: the launch arguments, copied to d_res per launch
+  ResArgs* d_res = nullptr;
+  ResLayer* d_layers = nullptr;
+  uint2* res_ex = nullptr;    // exchange pairs
+  size_t res_ex_bytes = 0;
+  ResCtl* res_ctl = nullptr;
+  ResCtl* h_ctl = nullptr;    // pinned read-back
+  uint32_t* h_ids = nullptr;  // pinned [RES_STEPS] ids of one launch
+  uint32_t res_epoch = 0;     // first epoch of the next launch
+  uint64_t* res_trace = nullptr;  // frn_resident_trace buffer
+  size_t res_trace_n = 0;         // its length in stamps
+  uint32_t res_trace_arm = 0;     // steps the next launch records
 };
 
 static void free_ctx(frn_ctx* c) {
@@ -136,6 +153,12 @@ static void free_ctx(frn_ctx* c) {
   if (c->h_hist) (void)hipHostFree(c->h_hist);
   if (c->h_recent) (void)hipHostFree(c->h_recent);
   if (c->h_rng) (void)hipHostFree(c->h_rng);
+  if (c->h_res) (void)hipHostFree(c->h_res);
+  if (c->h_ctl) (void)hipHostFree(c->h_ctl);
+  if (c->h_ids) (void)hipHostFree(c->h_ids);
+  void* rbufs[] = {c->d_res, c->d_layers, c->res_ex, c->res_ctl, c->res_trace};
+  for (void* p : rbufs)
+    if (p) (void)hipFree(p);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -159,6 +182,10 @@ constexpr uint32_t GREEDY_BATCH = 32;
 // decode steps per captured multi-step graph of frn_decode_greedy
 // (8 or 16 steps per graph measured the same: 1,100 tokens/s at 1.5B)
 constexpr uint32_t GREEDY_MULTI = 4;
+// decode steps per resident launch (one host synchronisation each)
+constexpr uint32_t RES_STEPS = 128;
+// whether models the resident kernel supports use it without FRN_FLAG_RESIDENT
+constexpr bool kResidentDefault = false;
 
 static hipError_t alloc_prefill(frn_ctx* x) {
   const frn_config& c = x->cfg;
@@ -485,6 +512,176 @@ static frn_status capture(frn_ctx* c, bool with_logits, hipGraph_t* graph, hipGr
   return FRN_OK;
 }
 
+// Decides whether the resident decode kernel serves this model and
+// prepares it: the per-layer weight table, the exchange buffers and the
+// launch arguments.  Unsupported shapes keep the step graphs (res_why).
+static frn_status setup_resident(frn_ctx* c) {
+  const frn_config& g = c->cfg;
+  c->res_ok = false;
+  if (g.flags & FRN_FLAG_NO_RESIDENT) {
+    c->res_why = "disabled by FRN_FLAG_NO_RESIDENT";
+    return FRN_OK;
+  }
+  if (!(g.flags & FRN_FLAG_RESIDENT) && !kResidentDefault) {
+    c->res_why = "the step graphs are the default (FRN_FLAG_RESIDENT selects the resident kernel)";
+    return FRN_OK;
+  }
+  if (g.flags & FRN_FLAG_EAGER) {
+    c->res_why = "FRN_FLAG_EAGER runs the step kernels one by one";
+    return FRN_OK;
+  }
+  hipDeviceProp_t prop;
+  int coop = 0;
+  HIP_TRY(hipGetDeviceProperties(&prop, c->device), "hipGetDeviceProperties");
+  HIP_TRY(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device), "hipDeviceGetAttribute");
+  if (prop.multiProcessorCount != (int)RES_BLOCKS || !coop) {
+    c->res_why = "needs 256 CUs and cooperative launches";
+    return FRN_OK;
+  }
+  std::vector<uint32_t> types;
+  uint32_t o_gran = 64;
+  for (const LayerPtrs& L : c->layers) {
+    for (const DevTensor* t : {L.wq, L.wk, L.wv, L.wo, L.gate, L.up, L.down}) types.push_back(t->type);
+    if (L.wo->type == T_Q6_K) o_gran = 128;
+  }
+  uint32_t fset = 0;
+  if (const char* why = res_unsupported(g.hidden, g.ffn, g.n_heads, g.n_kv_heads, g.head_dim, types.data(),
+                                        types.size(), c->lm_head->type, o_gran, &fset)) {
+    c->res_why = why;
+    return FRN_OK;
+  }
+  const ResLayout lay = res_layout(g.hidden, g.ffn, g.n_heads, g.n_kv_heads, g.head_dim);
+  c->res_ex_bytes = res_exchange_pairs(lay) * 8;
+  std::vector<ResLayer> tab(g.n_layers);
+  for (uint32_t l = 0; l < g.n_layers; ++l) {
+    const LayerPtrs& L = c->layers[l];
+    ResLayer& r = tab[l];
+    r.wq = L.wq->ptr; r.wk = L.wk->ptr; r.wv = L.wv->ptr; r.wo = L.wo->ptr;
+    r.wg = L.gate->ptr; r.wu = L.up->ptr; r.wd = L.down->ptr;
+    r.bq = L.bq; r.bk = L.bk; r.bv = L.bv; r.an = L.attn_norm; r.fn = L.ffn_norm;
+    r.tq = L.wq->type; r.tk = L.wk->type; r.tv = L.wv->type; r.to = L.wo->type; r.tg = L.gate->type;
+    r.td = L.down->type;
+    r.rq = (uint32_t)type_row_bytes(r.tq, L.wq->in); r.rk = (uint32_t)type_row_bytes(r.tk, L.wk->in);
+    r.rv = (uint32_t)type_row_bytes(r.tv, L.wv->in); r.ro = (uint32_t)type_row_bytes(r.to, L.wo->in);
+    r.rg = (uint32_t)type_row_bytes(r.tg, L.gate->in); r.rd = (uint32_t)type_row_bytes(r.td, L.down->in);
+  }
+  hipError_t e;
+  if ((e = dmalloc(&c->d_layers, tab.size() * sizeof(ResLayer))) || (e = dmalloc(&c->d_res, sizeof(ResArgs))) ||
+      (e = dmalloc(&c->res_ex, c->res_ex_bytes)) || (e = dmalloc(&c->res_ctl, sizeof(ResCtl))) ||
+      (e = hipHostMalloc((void**)&c->h_res, sizeof(ResArgs), hipHostMallocDefault)) ||
+      (e = hipHostMalloc((void**)&c->h_ctl, sizeof(ResCtl), hipHostMallocDefault)) ||
+      (e = hipHostMalloc((void**)&c->h_ids, RES_STEPS * 4, hipHostMallocDefault)) ||
+      (e = hipMemcpy(c->d_layers, tab.data(), tab.size() * sizeof(ResLayer), hipMemcpyHostToDevice)) ||
+      (e = hipMemset(c->res_ex, 0, c->res_ex_bytes)) || (e = res_prepare()))
+    return hip_fail(e, "resident decode setup");
+  ResArgs& a = *c->h_res;
+  memset(&a, 0, sizeof a);
+  a.layers = c->d_layers;
+  a.L = g.n_layers; a.H = g.hidden; a.F = g.ffn; a.nh = g.n_heads; a.nkv = g.n_kv_heads; a.hd = g.head_dim;
+  a.V = g.vocab; a.max_ctx = g.max_ctx;
+  a.eps = g.rms_eps;
+  a.scale = 1.0f / sqrtf((float)g.head_dim);  // model.rs:384
+  a.embd = c->embd->ptr; a.te = c->embd->type; a.rbe = (uint32_t)type_row_bytes(c->embd->type, g.hidden);
+  a.lm = c->lm_head->ptr; a.tl = c->lm_head->type; a.rbl = (uint32_t)type_row_bytes(c->lm_head->type, g.hidden);
+  a.onorm = c->out_norm;
+  a.kc = c->kcache; a.vc = c->vcache; a.rope = c->rope;
+  a.logits = c->logits; a.hist = c->hist; a.st = c->st;
+  a.loc = c->res_ex;
+  a.glb = c->res_ex + (size_t)RES_XCDS * 2 * lay.loc_stride;
+  a.lay = lay;
+  a.ctl = c->res_ctl;
+  a.fset = fset;
+  if (const char* o = getenv("FRN_RESIDENT_OPTS")) a.opts = (uint32_t)strtoul(o, nullptr, 0);
+  c->res_epoch = 0;
+  c->res_ok = true;
+  c->res_why = "";
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_resident_trace(frn_ctx* c, uint32_t n_steps, uint64_t* host_out, size_t n) {
+  if (!c) return fail(FRN_EINVAL, "frn_resident_trace: null context");
+  if (!c->res_ok) return fail(FRN_EINVAL, "frn_resident_trace: the resident decode kernel is not in use");
+  HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  const size_t need = (size_t)n_steps * (c->cfg.n_layers + 1) * RES_TR_K * RES_BLOCKS;
+  if (!host_out) {
+    if (need > c->res_trace_n) {
+      if (c->res_trace) HIP_TRY(hipFree(c->res_trace), "hipFree");
+      c->res_trace = nullptr;
+      c->res_trace_n = 0;
+      HIP_TRY(hipMalloc((void**)&c->res_trace, need * 8), "trace buffer");
+      c->res_trace_n = need;
+    }
+    if (need) HIP_TRY(hipMemset(c->res_trace, 0, need * 8), "trace clear");
+    c->res_trace_arm = n_steps;
+    return FRN_OK;
+  }
+  const size_t k = std::min(n, std::min(need, c->res_trace_n));
+  HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  if (k) HIP_TRY(hipMemcpy(host_out, c->res_trace, k * 8, hipMemcpyDeviceToHost), "trace copy");
+  return FRN_OK;
+}
+
+extern "C" frn_status frn_decode_engine(frn_ctx* c, uint32_t* resident, char* reason, size_t reason_len) {
+  if (!c || !resident) return fail(FRN_EINVAL, "frn_decode_engine: null argument");
+  *resident = c->res_ok ? 1u : 0u;
+  if (reason && reason_len) snprintf(reason, reason_len, "%s", c->res_why.c_str());
+  return FRN_OK;
+}
+
+// n greedy steps through resident launches of up to RES_STEPS steps; the
+// kernel itself stops after a step whose id is a stop id.  Ids go to out.
+static frn_status res_decode(frn_ctx* c, uint32_t id, uint32_t n, const uint32_t* stop_ids, uint32_t n_stop,
+                             uint32_t* out, uint32_t* n_done) {
+  const frn_config& g = c->cfg;
+  *n_done = 0;
+  if (id != c->last_next) {
+    c->h_st->tok = id;
+    HIP_TRY(hipMemcpyAsync((char*)c->st + offsetof(StepState, tok), &c->h_st->tok, 4, hipMemcpyHostToDevice, c->stream),
+            "token upload");
+  }
+  uint32_t done = 0;
+  while (done < n) {
+    const uint32_t b = std::min(n - done, RES_STEPS), p0 = c->len;
+    if ((uint64_t)c->res_epoch + res_epochs(b, g.n_layers) >= 0x7FFFFFFFull) {  // epochs restart on cleared pairs
+      HIP_TRY(hipMemsetAsync(c->res_ex, 0, c->res_ex_bytes, c->stream), "exchange reset");
+      c->res_epoch = 0;
+    }
+    ResArgs& a = *c->h_res;
+    a.n_steps = b;
+    a.n_stop = n_stop;
+    for (uint32_t k = 0; k < n_stop; ++k) a.stop[k] = stop_ids[k];
+    a.epoch0 = c->res_epoch;
+    c->res_epoch += res_epochs(b, g.n_layers);
+    a.trace = c->res_trace_arm ? c->res_trace : nullptr;
+    a.trace_steps = c->res_trace_arm;
+    c->res_trace_arm = 0;
+    HIP_TRY(launch_resident(c->h_res, c->d_res, c->stream), "resident decode launch");
+    HIP_TRY(hipMemcpyAsync(c->h_ctl, c->res_ctl, sizeof(ResCtl), hipMemcpyDeviceToHost, c->stream), "status read-back");
+    HIP_TRY(hipMemcpyAsync(c->h_ids, c->hist + p0, (size_t)b * 4, hipMemcpyDeviceToHost, c->stream), "id read-back");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    const uint32_t k = c->h_ctl->n_done;
+    if (c->h_ctl->err || k == 0 || k > b) {
+      const uint32_t err = c->h_ctl->err;
+      c->res_ok = false;
+      c->res_why = "a resident launch failed";
+      c->last_next = 0xFFFFFFFFu;
+      c->have_logits = false;
+      return fail(FRN_EHIP,
+                  "resident decode: %s (code %u, layer %u, phase %u); the context decodes with the step graphs from now on",
+                  (err >> 24) == (RES_ERR_LAYOUT >> 24) ? "blocks not spread 32 per XCD" : "a wait gave up",
+                  err >> 24, (err >> 8) & 0xFFFFu, err & 0xFFu);
+    }
+    memcpy(out + done, c->h_ids, (size_t)k * 4);
+    done += k;
+    c->len += k;
+    if (k < b) break;  // stopped at a stop id (generate.rs:125-127)
+  }
+  *n_done = done;
+  c->last_next = out[done - 1];
+  c->have_logits = true;
+  return FRN_OK;
+}
+
 extern "C" frn_status frn_finalize(frn_ctx* c) {
   if (!c) return fail(FRN_EINVAL, "frn_finalize: null context");
   if (c->finalized) return FRN_OK;
@@ -527,6 +724,7 @@ extern "C" frn_status frn_finalize(frn_ctx* c) {
       return fail(FRN_EDTYPE, "blk.%u: ffn_gate and ffn_up must share a type for the fused SwiGLU kernel", l);
   }
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  if ((st = setup_resident(c))) return st;
   if (!(g.flags & FRN_FLAG_EAGER)) {
     for (int lng = 0; lng < (g.max_ctx > ATTENTION_LONG_FROM ? 2 : 1); ++lng) {
       c->rec_long = lng;
@@ -683,6 +881,12 @@ extern "C" frn_status frn_decode(frn_ctx* c, uint32_t id, uint32_t* next_id) {
   if ((st = check_ready(c, 1))) return st;
   if (id >= c->cfg.vocab) return fail(FRN_ETOKEN, "token id %u out of range (vocab %u)", id, c->cfg.vocab);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  if (c->res_ok && !c->timing) {
+    uint32_t nxt = 0, k = 0;
+    if ((st = res_decode(c, id, 1, nullptr, 0, &nxt, &k))) return st;
+    if (next_id) *next_id = nxt;
+    return FRN_OK;
+  }
   uint32_t prev = c->last_next;
   c->last_next = prev;  // run_step skips the upload when id is the device's own argmax
   if ((st = run_step(c, id, true))) return st;
@@ -706,6 +910,13 @@ extern "C" frn_status frn_decode_greedy(frn_ctx* c, uint32_t id, uint32_t n, con
   if (n_stop && !stop_ids) return fail(FRN_EINVAL, "frn_decode_greedy: null stop_ids");
   if (id >= c->cfg.vocab) return fail(FRN_ETOKEN, "token id %u out of range (vocab %u)", id, c->cfg.vocab);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+  if (n == 0) return FRN_OK;
+  if (c->res_ok && !c->timing && n_stop <= RES_MAX_STOP) {
+    uint32_t k = 0;
+    st = res_decode(c, id, n, stop_ids, n_stop, out_ids, &k);
+    if (n_done) *n_done = k;
+    return st;
+  }
   uint32_t done = 0;
   bool stopped = false, rolled = false;
   while (done < n && !stopped) {

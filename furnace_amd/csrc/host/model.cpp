@@ -141,16 +141,25 @@ extern "C" frn_status frn_generate_greedy(frn_ctx* ctx, const uint32_t* prompt, 
   frn_status st = frn_prefill(ctx, prompt, n_prompt, &next);
   if (st) return st;
   s.prefill_s = now_s() - t0;
-  for (uint32_t step = 0; step < max_new; ++step) {
-    bool stop = false;
-    for (uint32_t i = 0; i < n_stop; ++i) stop |= stop_ids[i] == next;
-    if (stop) break;
+  auto is_stop = [&](uint32_t id) {
+    for (uint32_t i = 0; i < n_stop; ++i)
+      if (stop_ids[i] == id) return true;
+    return false;
+  };
+  // generate.rs:122-141: sample (the prefill's argmax), stop on eos/bos,
+  // push, then one forward per further token -- here all of them in one
+  // frn_decode_greedy call, which ends after a step whose argmax is a stop id
+  if (max_new > 0 && !is_stop(next)) {
     out_ids[s.n_generated++] = next;
-    if (step + 1 == max_new) break;
-    double t1 = now_s();
-    if ((st = frn_decode(ctx, next, &next))) return st;
-    s.decode_s += now_s() - t1;
-    s.decode_steps += 1;
+    if (max_new > 1) {
+      uint32_t done = 0;
+      double t1 = now_s();
+      if ((st = frn_decode_greedy(ctx, next, max_new - 1, stop_ids, n_stop, out_ids + 1, &done))) return st;
+      s.decode_s = now_s() - t1;
+      s.decode_steps = done;
+      s.n_generated += done;
+      if (done && is_stop(out_ids[done])) s.n_generated -= 1;  // the stop id is not pushed
+    }
   }
   if (stats) *stats = s;
   return FRN_OK;

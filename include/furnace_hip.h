@@ -59,6 +59,13 @@ typedef struct frn_config {
 /* Prefill one decode step per prompt position (the decode kernels) instead
  * of blocks of rows through the MFMA GEMMs.  For comparisons. */
 #define FRN_FLAG_STEPWISE_PREFILL 2u
+/* Decode with the per-step graphs even where the resident decode kernel
+ * (frn_decode_engine) could run.  For comparisons. */
+#define FRN_FLAG_NO_RESIDENT 4u
+/* Decode with the resident decode kernel where it can run (frn_decode_engine);
+ * without this flag or FRN_FLAG_NO_RESIDENT the engine picks the faster form
+ * for the model. */
+#define FRN_FLAG_RESIDENT 8u
 
 typedef struct frn_ctx frn_ctx;
 
@@ -108,6 +115,27 @@ frn_status frn_decode(frn_ctx* ctx, uint32_t id, uint32_t* next_id);
  * equal those of the frn_decode loop. */
 frn_status frn_decode_greedy(frn_ctx* ctx, uint32_t id, uint32_t n, const uint32_t* stop_ids, uint32_t n_stop,
                              uint32_t* out_ids, uint32_t* n_done);
+
+/* Which engine serves frn_decode / frn_decode_greedy (no counterpart in the
+ * reference, which has one CPU path): *resident = 1 for the resident decode
+ * kernel -- the whole greedy loop (every layer, lm_head, argmax, next
+ * embedding) in one persistent launch of one block per CU, the 8 XCDs each
+ * owning an eighth of the heads and of the FFN -- or 0 for the per-step
+ * graphs of kernels, with the reason in reason[0..reason_len) (may be NULL).
+ * The resident kernel needs an MI355X with 256 CUs, all matrices Q4_K/Q6_K
+ * or all Q8_0, hidden <= 4096 (a multiple of 256 for the K-quants), ffn a
+ * multiple of 128, head_dim 64 or 128.  A resident launch that fails (a
+ * bounded wait gave up) returns FRN_EHIP and the context decodes with the
+ * graphs from then on. */
+frn_status frn_decode_engine(frn_ctx* ctx, uint32_t* resident, char* reason, size_t reason_len);
+
+/* Profiling hook for the resident decode kernel (no counterpart in the
+ * reference).  host_out == NULL arms the next resident launch to record, for
+ * its first n_steps steps, a 100 MHz timestamp per block at the end of every
+ * phase: [n_steps][n_layers + 1][16][256] uint64 (layer n_layers: the
+ * lm_head, argmax and next embedding).  With host_out, copies the recorded
+ * stamps of the last armed launch (n values at most). */
+frn_status frn_resident_trace(frn_ctx* ctx, uint32_t n_steps, uint64_t* host_out, size_t n);
 
 /* Sampler::new (sampler.rs:68-78) on the device: temperature, top_k, top_p,
  * repeat penalty (1.0 disables) and the PCG32 seed (Pcg32::new).  At
