@@ -15,6 +15,7 @@
 #include <algorithm>
 #include <cmath>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1170,6 +1171,20 @@ extern "C" frn_status frn_bench_kernel(frn_ctx* c, const char* name, uint32_t la
 }
 
 // ---- single-op entry points ------------------------------------------------------
+namespace {
+// Per-device state the single-op entry points prepare on first use on a
+// device (the current device of the calling thread).
+constexpr int OP_MAX_DEVICES = 64;
+// argmax keys carry the index in 32 bits
+constexpr size_t ARGMAX_MAX_N = 0xFFFFFFFFull;
+struct OpDevice {
+  size_t gemv_lds = 0;             // dynamic LDS the GEMV kernels are prepared for
+  uint64_t* argmax_key = nullptr;  // frn_argmax's running key (allocated once)
+};
+std::mutex g_op_mu;
+OpDevice g_op_dev[OP_MAX_DEVICES];
+}  // namespace
+
 extern "C" frn_status frn_dequant(uint32_t type, const void* raw_dev, size_t raw_bytes, size_t n, float* out_dev,
                                   void* stream) {
   if (!known_type(type)) return fail(FRN_EDTYPE, "dequantization for type %u is not implemented", type);
@@ -1197,12 +1212,18 @@ extern "C" frn_status frn_matmul_quant(uint32_t type, const void* w_dev, size_t 
     return fail(FRN_EINVAL, "frn_matmul_quant: w_dev and a_dev must be 16-byte aligned");
   if (gemv_lds_bytes(d_in, false) > 160 * 1024)
     return fail(FRN_ESHAPE, "matmul: in dim %u exceeds the 160 KiB LDS staging limit", d_in);
-  static size_t prepared = 0;
-  if (gemv_lds_bytes(d_in, false) > prepared) {
-    HIP_TRY(gemv_prepare(gemv_lds_bytes(d_in, false)), "gemv_prepare");
-    prepared = gemv_lds_bytes(d_in, false);
-  }
   if (seq == 0 || d_out == 0) return FRN_OK;
+  {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= OP_MAX_DEVICES) return fail(FRN_EINVAL, "frn_matmul_quant: device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_op_mu);
+    const size_t need = gemv_lds_bytes(d_in, false);
+    if (need > g_op_dev[dev].gemv_lds) {
+      HIP_TRY(gemv_prepare(need), "gemv_prepare");
+      g_op_dev[dev].gemv_lds = need;
+    }
+  }
   for (uint32_t s = 0; s < seq; ++s) {
     GemvArgs a{};
     a.n_seg = 1;
@@ -1220,8 +1241,16 @@ extern "C" frn_status frn_matmul_quant(uint32_t type, const void* w_dev, size_t 
 
 extern "C" frn_status frn_argmax(const float* x_dev, size_t n, uint32_t* out_dev, void* stream) {
   if (!x_dev || !out_dev || n == 0) return fail(FRN_EINVAL, "frn_argmax: bad argument");
-  static thread_local uint64_t* scratch = nullptr;
-  if (!scratch) HIP_TRY(hipMalloc((void**)&scratch, 256), "argmax scratch");
-  HIP_TRY(launch_argmax(x_dev, n, scratch, out_dev, (hipStream_t)stream), "argmax launch");
+  if (n > ARGMAX_MAX_N) return fail(FRN_ESHAPE, "frn_argmax: %zu values exceed the 32-bit index limit", n);
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= OP_MAX_DEVICES) return fail(FRN_EINVAL, "frn_argmax: device %d out of range", dev);
+  uint64_t* key = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_op_mu);
+    if (!g_op_dev[dev].argmax_key) HIP_TRY(hipMalloc((void**)&g_op_dev[dev].argmax_key, 256), "argmax scratch");
+    key = g_op_dev[dev].argmax_key;
+  }
+  HIP_TRY(launch_argmax(x_dev, n, key, out_dev, (hipStream_t)stream), "argmax launch");
   return FRN_OK;
 }

@@ -214,12 +214,13 @@ frn_status frn_dequant(uint32_t type, const void* raw_dev, size_t raw_bytes, siz
 
 /* quant::matmul_quant (quant.rs:170-193): a_dev [seq, d_in] f32 times the
  * raw quantized weight w_dev [d_out, d_in] -> out_dev [seq, d_out] f32.
- * seq == 1 runs the decode GEMV kernel for `type`; seq > 1 the prefill
- * kernel.  w_bytes must equal d_out * (d_in / block) * block_bytes. */
+ * Each of the seq rows is one launch of the decode GEMV kernel for `type`.
+ * w_bytes must equal d_out * (d_in / block) * block_bytes. */
 frn_status frn_matmul_quant(uint32_t type, const void* w_dev, size_t w_bytes, const float* a_dev, uint32_t seq,
                             float* out_dev, uint32_t d_out, uint32_t d_in, void* stream);
 
-/* Device argmax over n floats, first maximum on ties (generate.rs:69-77). */
+/* Device argmax over n floats, first maximum on ties (generate.rs:69-77).
+ * n at most 2^32 - 1. */
 frn_status frn_argmax(const float* x_dev, size_t n, uint32_t* out_dev, void* stream);
 
 #ifdef __cplusplus
