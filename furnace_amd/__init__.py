@@ -88,6 +88,7 @@ SIGNATURES = {
     "frn_dequant": (_I, [_U32, _P, _SZ, _SZ, _P, _P]),
     "frn_matmul_quant": (_I, [_U32, _P, _SZ, _P, _U32, _P, _U32, _U32, _P]),
     "frn_argmax": (_I, [_P, _SZ, _P, _P]),
+    "frn_argmax_noalloc": (_I, [_P, _SZ, _P, _P]),
     "frn_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "frn_gguf_close": (None, [_P]),
     "frn_gguf_config": (_I, [_P, ctypes.POINTER(Config), ctypes.POINTER(_U32)]),

@@ -1180,6 +1180,7 @@ constexpr size_t ARGMAX_MAX_N = 0xFFFFFFFFull;
 struct OpDevice {
   size_t gemv_lds = 0;             // dynamic LDS the GEMV kernels are prepared for
   uint64_t* argmax_key = nullptr;  // frn_argmax's running key (allocated once)
+  uint64_t* scratch = nullptr;     // this device's copy of `scratch` (frn_argmax_noalloc)
 };
 std::mutex g_op_mu;
 OpDevice g_op_dev[OP_MAX_DEVICES];
@@ -1251,6 +1252,39 @@ extern "C" frn_status frn_argmax(const float* x_dev, size_t n, uint32_t* out_dev
     if (!g_op_dev[dev].argmax_key) HIP_TRY(hipMalloc((void**)&g_op_dev[dev].argmax_key, 256), "argmax scratch");
     key = g_op_dev[dev].argmax_key;
   }
+  HIP_TRY(launch_argmax(x_dev, n, key, out_dev, (hipStream_t)stream), "argmax launch");
+  return FRN_OK;
+}
+
+// frn_argmax_noalloc's scratch: a file-scope device array, one copy per GPU,
+// held until the process ends.  On the host its name is not a device
+// address: host code uses only the per-device address that
+// hipGetSymbolAddress returns (OpDevice::scratch).
+constexpr size_t NOALLOC_SCRATCH_BYTES = 256;
+static __device__ __align__(256) uint64_t scratch[NOALLOC_SCRATCH_BYTES / sizeof(uint64_t)];
+// argmax keeps one 64-bit running key there, for any n up to ARGMAX_MAX_N
+static_assert(sizeof(uint64_t) <= NOALLOC_SCRATCH_BYTES, "argmax key exceeds the scratch array");
+
+extern "C" frn_status frn_argmax_noalloc(const float* x_dev, size_t n, uint32_t* out_dev, void* stream) {
+  if (!x_dev || !out_dev || n == 0) return fail(FRN_EINVAL, "frn_argmax_noalloc: bad argument");
+  if (n > ARGMAX_MAX_N)
+    return fail(FRN_ESHAPE, "frn_argmax_noalloc: %zu values exceed the maximum of %zu (32-bit index)", n,
+                ARGMAX_MAX_N);
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= OP_MAX_DEVICES) return fail(FRN_EINVAL, "frn_argmax_noalloc: device %d out of range", dev);
+  uint64_t* key = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_op_mu);
+    if (!g_op_dev[dev].scratch) {
+      void* p = nullptr;
+      HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+      if (!p) return fail(FRN_EHIP, "frn_argmax_noalloc: no device address for the scratch array");
+      g_op_dev[dev].scratch = (uint64_t*)p;
+    }
+    key = g_op_dev[dev].scratch;
+  }
+  // the key is cleared by the first of the three launches (a kernel, no memset)
   HIP_TRY(launch_argmax(x_dev, n, key, out_dev, (hipStream_t)stream), "argmax launch");
   return FRN_OK;
 }

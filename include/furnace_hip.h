@@ -223,6 +223,15 @@ frn_status frn_matmul_quant(uint32_t type, const void* w_dev, size_t w_bytes, co
  * n at most 2^32 - 1. */
 frn_status frn_argmax(const float* x_dev, size_t n, uint32_t* out_dev, void* stream);
 
+/* frn_argmax without any allocation.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * result and limit (n at most 2^32 - 1, else FRN_ESHAPE) as frn_argmax; its
+ * 8-byte running key lives in a static 256-byte device array, one per GPU,
+ * looked up on the first call on each device.  Calls that overlap on one
+ * GPU (different streams or threads) share that array and race. */
+frn_status frn_argmax_noalloc(const float* x_dev, size_t n, uint32_t* out_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
