@@ -10,6 +10,7 @@ import argparse
 import ctypes
 import json
 import os
+import subprocess
 import sys
 import tempfile
 import time
@@ -61,16 +62,39 @@ def algorithmic_bytes(model):
     return w, kv_per_pos, per, lm
 
 
+def host_cpu():
+    """(logical cores this process may use, CPU model name)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    model = "unknown"
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.lower().startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    if model == "unknown" and os.path.exists("/proc/cpuinfo"):
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    return n, model
+
+
 def cpu_baseline(path, prompt, budget_s, threads):
     """The oracle (plain-C restatement of furnace's CPU path) on the host
-    cores: an 8-token prefill of the same model, then greedy decode steps
-    until about budget_s of decode work."""
+    cores, as generate.rs:109-141 runs it: the whole prompt as one prefill
+    forward (timed), then greedy decode steps until about budget_s of decode
+    work.  threads: the worker count (all logical cores unless
+    RAYON_NUM_THREADS says otherwise, as main.rs:167-176 chooses)."""
     from oracle import oracle as orc
     orc.set_threads(threads)
     m = orc.Model(path)
-    m.new_cache(512)
+    m.new_cache(len(prompt) + 300)
     t0 = time.perf_counter()
-    logits = m.forward_cached(prompt[:8])
+    logits = m.forward_cached(prompt)
     prefill_s = time.perf_counter() - t0
     tok = orc.argmax(logits)
     steps, dec = 0, 0.0
@@ -130,7 +154,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--seed", type=int, default=0xF0E1)
     ap.add_argument("--timing-steps", type=int, default=32, help="eager steps with per-kernel events")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="decode seconds of the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gguf", default=None, help="use this GGUF instead of writing the synthetic one")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one (for profilers) instead of "
@@ -271,13 +295,18 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
+        cores, cpu_model = host_cpu()
+        env = os.environ.get("RAYON_NUM_THREADS", "")
+        threads = int(env) if env.isdigit() and int(env) > 0 else cores
         tps, steps, dec, pf = cpu_baseline(path, prompt, args.cpu_seconds, threads)
-        log("cpu baseline: %.2f tokens/s (%d decode steps in %.1f s, %d threads; 8-token prefill %.1f s)" %
-            (tps, steps, dec, threads, pf))
+        log("cpu baseline (%s, %d logical cores, %d threads): %d-token prefill %.2f s (%.1f tokens/s); "
+            "decode %.2f tokens/s (%d steps in %.1f s)" %
+            (cpu_model, cores, threads, len(prompt), pf, len(prompt) / pf, tps, steps, dec))
         cpu = {"value": round(tps, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-               "sample": "oracle (C restatement of furnace's CPU path) on the same %s GGUF: 8-token prefill, "
-                         "then %d greedy decode steps" % (args.model, steps)}
+               "prefill_tokens_per_s": round(len(prompt) / pf, 2), "nproc": cores, "cpu_model": cpu_model,
+               "sample": "oracle (C restatement of furnace's CPU path) on the same %s GGUF: the %d-token prompt "
+                         "as one prefill forward, then %d greedy decode steps (%.1f s of decode)"
+                         % (args.model, len(prompt), steps, dec)}
     model.close()
     if not args.gguf:
         os.remove(path)

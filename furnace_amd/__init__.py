@@ -83,6 +83,8 @@ SIGNATURES = {
     "frn_last_error": (ctypes.c_char_p, []),
     "frn_timings_enable": (_I, [_P, _I]),
     "frn_timings_reset": (_I, [_P]),
+    "frn_step_times_enable": (_I, [_P, ctypes.c_int]),
+    "frn_step_times": (_I, [_P, _P, _U32, ctypes.POINTER(_U32)]),
     "frn_timings": (_I, [_P, ctypes.POINTER(Timing), _U32, ctypes.POINTER(_U32)]),
     "frn_bench_kernel": (_I, [_P, ctypes.c_char_p, _U32, _U32, ctypes.POINTER(ctypes.c_float)]),
     "frn_dequant": (_I, [_U32, _P, _SZ, _SZ, _P, _P]),
@@ -393,6 +395,16 @@ class Model:
         n = ctypes.c_uint32()
         check(load().frn_timings(self.ctx, arr, 32, ctypes.byref(n)))
         return {arr[i].name.decode(): (arr[i].ms, arr[i].calls) for i in range(n.value)}
+
+    def step_times_enable(self, on=True):
+        check(load().frn_step_times_enable(self.ctx, 1 if on else 0))
+
+    def step_times(self, max_n=1 << 16):
+        """Per-step decode durations (ms) kept since the last read."""
+        arr = (ctypes.c_float * max_n)()
+        n = ctypes.c_uint32()
+        check(load().frn_step_times(self.ctx, arr, max_n, ctypes.byref(n)))
+        return list(arr[:n.value])
 
     def bench_kernel(self, name, layer=None, reps=10):
         """Mean time per launch (us) of one kernel category replayed back to

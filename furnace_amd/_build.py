@@ -2,7 +2,10 @@
 
 Outputs, in-tree so they travel with the repository snapshot:
   furnace_amd/lib/libfurnace_hip.so   kernels for gfx950, C ABI, host side
+  furnace_amd/lib/libfurnace_hip.a    the same objects as a static library
   furnace_amd/bin/furnace-hip         CLI (run / dump-tensor / synth)
+  furnace_amd/bin/capi_static         tests/capi_static.c linked statically
+                                      against libfurnace_hip.a
 Objects go to furnace_amd/_build/.
 """
 import os
@@ -15,6 +18,9 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "lib", "libfurnace_hip.so")
 CLI = os.path.join(PKG, "bin", "furnace-hip")
+STATIC = os.path.join(PKG, "lib", "libfurnace_hip.a")
+CAPI_STATIC = os.path.join(PKG, "bin", "capi_static")
+TESTS = os.path.join(os.path.dirname(PKG), "tests")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # packed-fp32 instructions are disabled for all device code: some of their
@@ -58,9 +64,18 @@ def build(verbose=False):
     tmp = LIB + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", "-o", tmp] + objs + ["-lpthread"])
     os.replace(tmp, LIB)
+    tmp = STATIC + ".tmp"
+    if os.path.exists(tmp):
+        os.remove(tmp)
+    _run(["ar", "rcs", tmp] + objs)
+    os.replace(tmp, STATIC)
     _run(["g++"] + CXX_FLAGS + [os.path.join(CSRC, "host", "cli.cpp"), "-o", CLI,
           "-L" + os.path.dirname(LIB), "-lfurnace_hip", "-L/opt/rocm/lib", "-lamdhip64",
           "-Wl,-rpath,$ORIGIN/../lib", "-Wl,-rpath,/opt/rocm/lib"])
+    # a C caller linked against the archive (no libfurnace_hip.so at run time)
+    cobj = os.path.join(BUILD, "capi_static.o")
+    _run(["gcc", "-O2", "-std=c99", "-Wall", "-Wextra", "-c", os.path.join(TESTS, "capi_static.c"), "-o", cobj])
+    _run([HIPCC, "-o", CAPI_STATIC, cobj, STATIC, "-lpthread", "-Wl,-rpath,/opt/rocm/lib"])
     return LIB
 
 

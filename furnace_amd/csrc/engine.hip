@@ -118,6 +118,10 @@ struct frn_ctx {
   std::vector<int> ev_cat;
   double t_ms[N_CAT] = {0};
   uint64_t t_calls[N_CAT] = {0};
+  // frn_step_times: an event after every decode step, durations kept here
+  bool step_timing = false;
+  std::vector<hipEvent_t> st_ev;  // GREEDY_BATCH + 1
+  std::vector<float> step_ms;
   // resident decode (resident.hip): the whole greedy loop in one launch
   bool res_ok = false;
   std::string res_why = "not finalized";
@@ -147,6 +151,7 @@ static void free_ctx(frn_ctx* c) {
   }
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+  for (hipEvent_t e : c->st_ev) (void)hipEventDestroy(e);
   void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.keys_sorted, c->full.ids, c->full.ids_sorted, c->full.tmp, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
@@ -882,16 +887,23 @@ extern "C" frn_status frn_decode(frn_ctx* c, uint32_t id, uint32_t* next_id) {
   if ((st = check_ready(c, 1))) return st;
   if (id >= c->cfg.vocab) return fail(FRN_ETOKEN, "token id %u out of range (vocab %u)", id, c->cfg.vocab);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
-  if (c->res_ok && !c->timing) {
+  if (c->res_ok && !c->timing && !c->step_timing) {
     uint32_t nxt = 0, k = 0;
     if ((st = res_decode(c, id, 1, nullptr, 0, &nxt, &k))) return st;
     if (next_id) *next_id = nxt;
     return FRN_OK;
   }
-  uint32_t prev = c->last_next;
-  c->last_next = prev;  // run_step skips the upload when id is the device's own argmax
+  if (c->step_timing) HIP_TRY(hipEventRecord(c->st_ev[0], c->stream), "hipEventRecord");
+  // run_step skips the upload when id is the device's own argmax
   if ((st = run_step(c, id, true))) return st;
-  return read_next(c, next_id);
+  if (c->step_timing) HIP_TRY(hipEventRecord(c->st_ev[1], c->stream), "hipEventRecord");
+  if ((st = read_next(c, next_id))) return st;
+  if (c->step_timing) {
+    float ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&ms, c->st_ev[0], c->st_ev[1]), "hipEventElapsedTime");
+    c->step_ms.push_back(ms);
+  }
+  return FRN_OK;
 }
 
 // Greedy decode without a host round trip per step (generate.rs:110-136 at
@@ -912,7 +924,7 @@ extern "C" frn_status frn_decode_greedy(frn_ctx* c, uint32_t id, uint32_t n, con
   if (id >= c->cfg.vocab) return fail(FRN_ETOKEN, "token id %u out of range (vocab %u)", id, c->cfg.vocab);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
   if (n == 0) return FRN_OK;
-  if (c->res_ok && !c->timing && n_stop <= RES_MAX_STOP) {
+  if (c->res_ok && !c->timing && !c->step_timing && n_stop <= RES_MAX_STOP) {
     uint32_t k = 0;
     st = res_decode(c, id, n, stop_ids, n_stop, out_ids, &k);
     if (n_done) *n_done = k;
@@ -922,11 +934,14 @@ extern "C" frn_status frn_decode_greedy(frn_ctx* c, uint32_t id, uint32_t n, con
   bool stopped = false, rolled = false;
   while (done < n && !stopped) {
     const uint32_t b = std::min<uint32_t>(n - done, GREEDY_BATCH), p0 = c->len;
+    if (c->step_timing) HIP_TRY(hipEventRecord(c->st_ev[0], c->stream), "hipEventRecord");
     for (uint32_t i = 0; i < b;) {
       // GREEDY_MULTI steps in one graph when the token is already on the
-      // device and all of them run the same attention form
+      // device and all of them run the same attention form (one graph per
+      // step while step times are recorded)
       const bool same_form = (c->len + 1 > ATTENTION_LONG_FROM) == (c->len + GREEDY_MULTI > ATTENTION_LONG_FROM);
-      if (done + i > 0 && b - i >= GREEDY_MULTI && same_form && !c->timing && !(c->cfg.flags & FRN_FLAG_EAGER)) {
+      if (done + i > 0 && b - i >= GREEDY_MULTI && same_form && !c->timing && !c->step_timing &&
+          !(c->cfg.flags & FRN_FLAG_EAGER)) {
         c->rec_long = c->len + 1 > ATTENTION_LONG_FROM;
         HIP_TRY(hipGraphLaunch(c->g_multi[c->rec_long], c->stream), "hipGraphLaunch");
         c->len += GREEDY_MULTI;
@@ -935,6 +950,7 @@ extern "C" frn_status frn_decode_greedy(frn_ctx* c, uint32_t id, uint32_t n, con
         continue;
       }
       if ((st = run_step(c, id, true, done + i > 0))) return st;
+      if (c->step_timing) HIP_TRY(hipEventRecord(c->st_ev[i + 1], c->stream), "hipEventRecord");
       ++i;
     }
     HIP_TRY(hipMemcpyAsync(c->h_hist, c->hist + p0, (size_t)b * 4, hipMemcpyDeviceToHost, c->stream),
@@ -948,6 +964,11 @@ extern "C" frn_status frn_decode_greedy(frn_ctx* c, uint32_t id, uint32_t n, con
           stopped = true;
           used = i + 1;
         }
+    }
+    for (uint32_t i = 0; c->step_timing && i < used; ++i) {
+      float ms = 0.f;
+      HIP_TRY(hipEventElapsedTime(&ms, c->st_ev[i], c->st_ev[i + 1]), "hipEventElapsedTime");
+      c->step_ms.push_back(ms);
     }
     done += used;
     if (used < b) {  // roll the position back to just after the stop id's step
@@ -1120,6 +1141,28 @@ extern "C" frn_status frn_timings_reset(frn_ctx* c) {
   if (!c) return fail(FRN_EINVAL, "null context");
   memset(c->t_ms, 0, sizeof c->t_ms);
   memset(c->t_calls, 0, sizeof c->t_calls);
+  return FRN_OK;
+}
+extern "C" frn_status frn_step_times_enable(frn_ctx* c, int enable) {
+  if (!c) return fail(FRN_EINVAL, "null context");
+  if (enable && c->st_ev.empty()) {
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    for (uint32_t i = 0; i <= GREEDY_BATCH; ++i) {
+      hipEvent_t e;
+      HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+      c->st_ev.push_back(e);
+    }
+  }
+  c->step_timing = enable != 0;
+  c->step_ms.clear();
+  return FRN_OK;
+}
+extern "C" frn_status frn_step_times(frn_ctx* c, float* ms_out, uint32_t max, uint32_t* n) {
+  if (!c || !n || (max && !ms_out)) return fail(FRN_EINVAL, "frn_step_times: null argument");
+  const uint32_t k = (uint32_t)std::min<size_t>(max, c->step_ms.size());
+  std::copy(c->step_ms.begin(), c->step_ms.begin() + k, ms_out);
+  c->step_ms.erase(c->step_ms.begin(), c->step_ms.begin() + k);
+  *n = k;
   return FRN_OK;
 }
 extern "C" frn_status frn_timings(frn_ctx* c, frn_timing* out, uint32_t max, uint32_t* n) {

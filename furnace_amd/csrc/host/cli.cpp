@@ -8,6 +8,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
+#include <unistd.h>
 
 #include <string>
 #include <vector>
@@ -92,25 +93,55 @@ static int cmd_run(int argc, char** argv) {
   size_t kv_bytes = 2ull * cfg.n_layers * max_ctx * cfg.n_kv_heads * cfg.head_dim * 4;
   fprintf(stderr, "kv cache: %.0f MB for %u positions\n", kv_bytes / (1024.0 * 1024.0), max_ctx);
   frn_timings_enable(ctx, timings);
+  if (frn_step_times_enable(ctx, 1)) return die("step times");
   std::vector<uint32_t> out(max_new);
   frn_gen_stats st;
   uint64_t draws = 0;
-  if (temp == 0.0f) {
+  if (!have_seed) {  // main.rs:253-259: clock nanoseconds xor the process id
+    struct timespec ts;
+    clock_gettime(CLOCK_REALTIME, &ts);
+    seed = ((uint64_t)ts.tv_sec * 1000000000ull + (uint64_t)ts.tv_nsec) ^ (uint64_t)getpid();
+  }
+  fprintf(stderr, "sampler: temp %g top-k %u top-p %g repeat-penalty %g seed %llu\n", (double)temp, top_k,
+          (double)top_p, (double)repeat_penalty, (unsigned long long)seed);
+  // Sampler::sample at temperature 0 is the argmax of the penalized logits
+  // (sampler.rs:86-108); without a penalty that is the plain argmax, which
+  // the device loop feeds back step to step with no host round trip
+  if (temp == 0.0f && repeat_penalty == 1.0f) {
     if (frn_generate_greedy(ctx, ids.data(), (uint32_t)ids.size(), max_new, stop, n_stop, out.data(), &st))
       return die("generate");
   } else {
-    if (!have_seed) seed = (uint64_t)time(nullptr);  // main.rs:253-259: one drawn from the clock
-    fprintf(stderr, "sampler: temp %g top-k %u top-p %g repeat-penalty %g seed %llu\n", (double)temp, top_k,
-            (double)top_p, (double)repeat_penalty, (unsigned long long)seed);
     if (frn_generate_sampled(ctx, ids.data(), (uint32_t)ids.size(), max_new, temp, top_k, top_p, repeat_penalty,
                              seed, stop, n_stop, out.data(), &st, &draws))
       return die("generate");
   }
-  fprintf(stderr, "prefill: %zu tokens in %.2f s (%.2f ms/token)\n", ids.size(), st.prefill_s,
+  fprintf(stderr, "prefill: %zu tokens in %.3f s (%.3f ms/token)\n", ids.size(), st.prefill_s,
           st.prefill_s * 1000.0 / ids.size());
+  // generate.rs:137-140: one line per decode forward, the cache length after it
+  std::vector<float> step_ms(st.decode_steps ? st.decode_steps : 1);
+  uint32_t n_ms = 0;
+  if (frn_step_times(ctx, step_ms.data(), (uint32_t)step_ms.size(), &n_ms)) return die("step times");
+  for (uint32_t k = 0; k < n_ms; ++k)
+    fprintf(stderr, "[decode %3u: seq %4zu, %8.3f ms/token]\n", k, ids.size() + k + 1, (double)step_ms[k]);
   if (st.decode_steps)
     fprintf(stderr, "decode: %u steps, %.3f ms/token average (%.1f tokens/s)\n", st.decode_steps,
             st.decode_s * 1000.0 / st.decode_steps, st.decode_steps / st.decode_s);
+  if (timings) {  // perf.rs:69-96 over the decode phase (reset after the prefill)
+    const double wall = st.decode_s * 1000.0;
+    frn_timing t[32];
+    uint32_t nt = 0;
+    if (frn_timings(ctx, t, 32, &nt)) return die("timings");
+    fprintf(stderr, "decode op breakdown (%.3f ms wall):\n", wall);
+    double accounted = 0.0;
+    for (uint32_t i = 0; i < nt; ++i) {
+      if (!t[i].calls) continue;
+      accounted += t[i].ms;
+      fprintf(stderr, "  %-12s %9.3f ms  %5.1f%%  %7llu calls\n", t[i].name, t[i].ms,
+              wall > 0 ? 100.0 * t[i].ms / wall : 0.0, (unsigned long long)t[i].calls);
+    }
+    fprintf(stderr, "  %-12s %9.3f ms  %5.1f%%\n", "unaccounted", wall - accounted,
+            wall > 0 ? 100.0 * (wall - accounted) / wall : 0.0);
+  }
   fprintf(stderr, "sampler: %llu RNG draws\n", (unsigned long long)draws);
   fprintf(stderr, "generated ids: [");
   for (uint32_t i = 0; i < st.n_generated; ++i) fprintf(stderr, "%s%u", i ? ", " : "", out[i]);

@@ -141,6 +141,7 @@ extern "C" frn_status frn_generate_greedy(frn_ctx* ctx, const uint32_t* prompt, 
   frn_status st = frn_prefill(ctx, prompt, n_prompt, &next);
   if (st) return st;
   s.prefill_s = now_s() - t0;
+  if ((st = frn_timings_reset(ctx))) return st;  // generate.rs:119: the breakdown covers decode only
   auto is_stop = [&](uint32_t id) {
     for (uint32_t i = 0; i < n_stop; ++i)
       if (stop_ids[i] == id) return true;
@@ -179,6 +180,7 @@ extern "C" frn_status frn_generate_sampled(frn_ctx* ctx, const uint32_t* prompt,
   double t0 = now_s();
   if ((st = frn_prefill(ctx, prompt, n_prompt, &next))) return st;
   s.prefill_s = now_s() - t0;
+  if ((st = frn_timings_reset(ctx))) return st;  // generate.rs:119: the breakdown covers decode only
   for (uint32_t step = 0; step < max_new; ++step) {
     const size_t w = context.size() > window ? context.size() - window : 0;  // generate.rs:123
     if ((st = frn_sample(ctx, context.data() + w, (uint32_t)(context.size() - w), &next))) return st;

@@ -192,6 +192,17 @@ frn_status frn_timings_enable(frn_ctx* ctx, int enable);
 frn_status frn_timings_reset(frn_ctx* ctx);
 frn_status frn_timings(frn_ctx* ctx, frn_timing* out, uint32_t max, uint32_t* n);
 
+/* Per-step decode times, for the `[decode N: seq M, X ms/token]` lines of
+ * generate.rs:137-140.  While enabled, frn_decode and frn_decode_greedy
+ * record a HIP event after every step (one graph launch per step; the
+ * resident decode kernel is not used) and keep each step's duration in ms:
+ * from the end of the previous step of the same batch (the batch's start
+ * for its first step) to the step's end.  Enabling (or disabling) forgets
+ * what was kept.  frn_step_times moves up to max kept durations, oldest
+ * first, to ms_out; *n receives the count. */
+frn_status frn_step_times_enable(frn_ctx* ctx, int enable);
+frn_status frn_step_times(frn_ctx* ctx, float* ms_out, uint32_t max, uint32_t* n);
+
 /* Measurement hook (no counterpart in the reference; used by the bench to
  * price one kernel without per-launch event overhead): launches the kernel
  * of timing category `name` (as in frn_timings) for `layer` `reps` times
