@@ -44,6 +44,8 @@ void orc_rmsnorm(const float* x, size_t rows, size_t cols, const float* w, float
 /* tensor.rs:188-203: fold(-inf, f32::max), exp(v - max), sequential sum
  * from 0.0, divide. */
 void orc_softmax(float* x, size_t rows, size_t cols) {
+  /* rows are independent: threads split them, each row's order unchanged */
+#pragma omp parallel for schedule(static) if (rows * cols > (1u << 16))
   for (size_t r = 0; r < rows; ++r) {
     float* row = x + r * cols;
     float mx = -INFINITY;
@@ -105,9 +107,11 @@ void orc_attention_scores_cached(const float* q, size_t n_new, const float* k_ca
                                  size_t start_pos, size_t nh, size_t nkv, size_t hd, float* probs) {
   size_t kv_dim = nkv * hd, group = nh / nkv;
   float scale = 1.0f / sqrtf((float)hd);
+  /* (head, row) pairs are independent: threads split them, each dot's order unchanged */
+#pragma omp parallel for collapse(2) schedule(static) if (nh * n_new * total > (1u << 16))
   for (size_t h = 0; h < nh; ++h) {
-    size_t kv = h / group;
     for (size_t s = 0; s < n_new; ++s) {
+      size_t kv = h / group;
       const float* qh = q + s * nh * hd + h * hd;
       float* row = probs + (h * n_new + s) * total;
       for (size_t t = 0; t < total; ++t)
@@ -122,9 +126,11 @@ void orc_attention_apply_cached(const float* probs, size_t n_new, size_t total, 
                                 size_t nh, size_t nkv, size_t hd, float* out) {
   size_t kv_dim = nkv * hd, group = nh / nkv;
   memset(out, 0, n_new * nh * hd * sizeof(float));
+  /* each (head, row) pair writes its own output row: threads split them */
+#pragma omp parallel for collapse(2) schedule(static) if (nh * n_new * total > (1u << 16))
   for (size_t h = 0; h < nh; ++h) {
-    size_t kv = h / group;
     for (size_t s = 0; s < n_new; ++s) {
+      size_t kv = h / group;
       const float* row = probs + (h * n_new + s) * total;
       float* oh = out + s * nh * hd + h * hd;
       for (size_t t = 0; t < total; ++t) {

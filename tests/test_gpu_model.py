@@ -169,6 +169,76 @@ def test_long_context_small_model(hip, tmpdir_models):
     ref.close()
 
 
+def test_long_context_1p5b_head_shape(hip, tmpdir_models):
+    """The long-context form at the Qwen2-1.5B head shape (12 query heads
+    over 2 kv heads, head_dim 128; model.rs:371-438) against the oracle:
+    a 4200-token prompt through the prefill's row blocks, then 8 decode
+    steps whose attention runs past 4096 positions in up to 128 splits per
+    head, merged per head.  Two layers, FFN 1280 and a 2048-id vocabulary
+    keep the oracle's run to seconds."""
+    cfg = dict(n_layers=2, n_heads=12, n_kv_heads=2, hidden=1536, ffn=1280, vocab=2048, mix=fa.MIX_Q4_K_M,
+               tied=1, embd_type=fa.Q6_K, output_type=fa.Q6_K)
+    path = os.path.join(tmpdir_models, "hd128-long.gguf")
+    fa.synth_write(path, seed=37, **cfg)
+    prompt = np.random.default_rng(37).integers(0, cfg["vocab"], 4200).astype(np.uint32)
+    orc.set_threads(min(16, os.cpu_count() or 1))
+    print("1.5B head shape, prompt %d: oracle prefill" % prompt.size, flush=True)
+    ref = orc.Model(path)
+    ref.new_cache(4300)
+    ref_logits = ref.forward_cached(prompt)
+    print("device prefill", flush=True)
+    m = fa.Model(path, max_ctx=4300)
+    nxt = m.prefill(prompt)
+    assert np.max(np.abs(m.logits() - ref_logits)) <= LOGIT_TOL
+    tok = orc.argmax(ref_logits)
+    assert nxt == tok
+    for step in range(8):
+        ref_logits = ref.forward_cached([tok])
+        nxt = m.decode(tok)
+        assert np.max(np.abs(m.logits() - ref_logits)) <= LOGIT_TOL, step
+        assert nxt == orc.argmax(ref_logits), step
+        tok = nxt
+    m.close()
+    ref.close()
+    os.remove(path)
+
+
+def test_7b_shape_prompt_scale_prefill(hip, tmpdir_models):
+    """The Qwen2-7B layer shapes (hidden 3584, FFN 18944, 7 query heads per
+    kv head, untied Q6_K lm_head [152064, 3584]) at prompt scale: a
+    640-token prompt runs the prefill's 128-row GEMM tiles at their real K
+    (3584 and 18944; tensor.rs:114-135), then 8 greedy decode steps, all
+    against the oracle.  Two layers keep the oracle's run to about half a
+    minute."""
+    cfg = dict(fa.PRESETS["qwen2-7b-q4_k_m"], n_layers=2)
+    path = os.path.join(tmpdir_models, "qwen2-7b-2layer.gguf")
+    print("writing 2-layer 7b-shape model", flush=True)
+    fa.synth_write(path, seed=41, threads=min(16, os.cpu_count() or 1), **cfg)
+    prompt = np.random.default_rng(41).integers(0, 151643, 640).astype(np.uint32)
+    orc.set_threads(min(16, os.cpu_count() or 1))
+    print("7b shape, prompt %d: oracle prefill" % prompt.size, flush=True)
+    ref = orc.Model(path)
+    ref.new_cache(700)
+    ref_logits = ref.forward_cached(prompt)
+    print("device prefill", flush=True)
+    m = fa.Model(path, max_ctx=700)
+    nxt = m.prefill(prompt)
+    assert np.max(np.abs(m.logits() - ref_logits)) <= LOGIT_TOL
+    tok = orc.argmax(ref_logits)
+    assert nxt == tok
+    ids, ref_ids = [], []
+    for step in range(8):
+        ref_logits = ref.forward_cached([tok])
+        ref_ids.append(orc.argmax(ref_logits))
+        ids.append(m.decode(tok))
+        assert np.max(np.abs(m.logits() - ref_logits)) <= LOGIT_TOL, step
+        tok = ref_ids[-1]
+    assert ids == ref_ids
+    m.close()
+    ref.close()
+    os.remove(path)
+
+
 def test_long_context_full_size_paths_agree(hip, tmpdir_models):
     """The long-context workload's shape (1.5B Q4_K_M, 4096-token prompt) is
     beyond the oracle's reach in a test, so the two device paths are
