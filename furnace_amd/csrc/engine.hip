@@ -101,8 +101,9 @@ struct frn_ctx {
   SamplerFull full;     // its buffers, allocated by the first frn_sampler_init that needs them
   // prefill rows: blocks of up to pf_rows prompt tokens through all layers
   uint32_t pf_rows = 0;
-  float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr, *pf_att = nullptr, *pf_act = nullptr,
-        *pf_inv = nullptr;
+  float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
+  // the GEMM operands as bf16 hi + lo planes: rmsnorm'd x, attention rows, SwiGLU activation
+  uint16_t *pf_xs = nullptr, *pf_att = nullptr, *pf_act = nullptr;
   uint32_t* pf_ids = nullptr;
   uint32_t len = 0;           // host view of KvCache::len
   uint32_t last_next = 0xFFFFFFFFu;
@@ -152,7 +153,7 @@ static void free_ctx(frn_ctx* c) {
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->st_ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.keys_sorted, c->full.ids, c->full.ids_sorted, c->full.tmp, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_att, c->pf_act, c->pf_inv, c->pf_ids};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.keys_sorted, c->full.ids, c->full.ids_sorted, c->full.tmp, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_ids};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -201,8 +202,8 @@ static hipError_t alloc_prefill(frn_ctx* x) {
   hipError_t e;
   if ((e = dmalloc(&x->pf_x, P * c.hidden * 4)) || (e = dmalloc(&x->pf_q, P * qd * 4)) ||
       (e = dmalloc(&x->pf_k, P * kvd * 4)) || (e = dmalloc(&x->pf_v, P * kvd * 4)) ||
-      (e = dmalloc(&x->pf_att, P * qd * 4)) || (e = dmalloc(&x->pf_act, P * c.ffn * 4)) ||
-      (e = dmalloc(&x->pf_inv, P * 4)) || (e = dmalloc(&x->pf_ids, P * 4)))
+      (e = dmalloc(&x->pf_xs, P * c.hidden * 4)) || (e = dmalloc(&x->pf_att, P * qd * 4)) ||
+      (e = dmalloc(&x->pf_act, P * c.ffn * 4)) || (e = dmalloc(&x->pf_ids, P * 4)))
     return e;
   return hipSuccess;
 }
@@ -276,7 +277,8 @@ extern "C" frn_status frn_create(const frn_config* cfg, int device, frn_ctx** ou
       (e = hipMemcpy(x->st, &init, sizeof init, hipMemcpyHostToDevice)) ||
       (e = hipMemset(x->kcache, 0, kv_bytes)) || (e = hipMemset(x->vcache, 0, kv_bytes)) ||
       (e = gemv_prepare(std::max(gemv_lds_bytes(c.hidden, true),
-                                 std::max(gemv_lds_bytes(c.ffn, false), gemv_lds_bytes(c.n_heads * c.head_dim, false)))))) {
+                                 std::max(gemv_lds_bytes(c.ffn, false), gemv_lds_bytes(c.n_heads * c.head_dim, false))))) ||
+      (e = gemm_prepare())) {
     free_ctx(x);
     return hip_fail(e, "frn_create: init");
   }
@@ -807,18 +809,21 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
     if ((e = launch_embed_rows(c->embd->ptr, c->embd->type, H, (uint32_t)type_row_bytes(c->embd->type, H), c->pf_ids,
                                m, c->pf_x, s)))
       return e;
-    auto gemm = [&](const DevTensor* w, const DevTensor* w2, const float* a, uint32_t K, const float* norm,
-                    const float* bias, float* out, uint32_t ldo, GemmMode mode) {
+    // the planes of an operand [m][K]: hi first, lo after
+    auto lo_of = [&](uint16_t* hi, uint32_t K) { return hi + (size_t)m * K; };
+    auto gemm = [&](const DevTensor* w, const DevTensor* w2, uint16_t* a, uint32_t K, const float* bias, float* out,
+                    uint16_t* o_planes, uint32_t ldo, GemmMode mode) {
       GemmArgs ga{};
-      ga.a = a;
-      ga.inv = norm ? c->pf_inv : nullptr;
-      ga.nw = norm;
+      ga.a_hi = a;
+      ga.a_lo = lo_of(a, K);
       ga.w = w->ptr;
       ga.w2 = w2 ? w2->ptr : nullptr;
       ga.type = w->type;
       ga.row_bytes = (uint32_t)type_row_bytes(w->type, w->in);
       ga.bias = bias;
       ga.out = out;
+      ga.o_hi = o_planes;
+      ga.o_lo = o_planes ? lo_of(o_planes, ldo) : nullptr;
       ga.ldo = ldo;
       ga.P = m;
       ga.N = (uint32_t)w->out;
@@ -828,18 +833,18 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
     for (uint32_t l = 0; l < g.n_layers; ++l) {
       const LayerPtrs& L = c->layers[l];
       const size_t lo = (size_t)l * g.max_ctx * KVD;
-      if ((e = launch_row_inv(c->pf_x, m, H, g.rms_eps, c->pf_inv, s)) ||
-          (e = gemm(L.wq, nullptr, c->pf_x, H, L.attn_norm, L.bq, c->pf_q, QD, GEMM_STORE)) ||
-          (e = gemm(L.wk, nullptr, c->pf_x, H, L.attn_norm, L.bk, c->pf_k, KVD, GEMM_STORE)) ||
-          (e = gemm(L.wv, nullptr, c->pf_x, H, L.attn_norm, L.bv, c->pf_v, KVD, GEMM_STORE)) ||
+      if ((e = launch_rows_split(c->pf_x, m, H, L.attn_norm, g.rms_eps, c->pf_xs, lo_of(c->pf_xs, H), s)) ||
+          (e = gemm(L.wq, nullptr, c->pf_xs, H, L.bq, c->pf_q, nullptr, QD, GEMM_STORE)) ||
+          (e = gemm(L.wk, nullptr, c->pf_xs, H, L.bk, c->pf_k, nullptr, KVD, GEMM_STORE)) ||
+          (e = gemm(L.wv, nullptr, c->pf_xs, H, L.bv, c->pf_v, nullptr, KVD, GEMM_STORE)) ||
           (e = launch_rope_kv_rows(c->pf_q, c->pf_k, c->pf_v, c->rope, c->kcache + lo, c->vcache + lo, g.n_heads,
                                    g.n_kv_heads, g.head_dim, pos0, m, s)) ||
-          (e = launch_attn_rows(c->pf_q, c->kcache + lo, c->vcache + lo, c->pf_att, g.n_heads, g.n_kv_heads,
-                                g.head_dim, pos0, m, scale, s)) ||
-          (e = gemm(L.wo, nullptr, c->pf_att, QD, nullptr, nullptr, c->pf_x, H, GEMM_RESID)) ||
-          (e = launch_row_inv(c->pf_x, m, H, g.rms_eps, c->pf_inv, s)) ||
-          (e = gemm(L.gate, L.up, c->pf_x, H, L.ffn_norm, nullptr, c->pf_act, g.ffn, GEMM_SWIGLU)) ||
-          (e = gemm(L.down, nullptr, c->pf_act, g.ffn, nullptr, nullptr, c->pf_x, H, GEMM_RESID)))
+          (e = launch_attn_rows(c->pf_q, c->kcache + lo, c->vcache + lo, c->pf_att, lo_of(c->pf_att, QD), g.n_heads,
+                                g.n_kv_heads, g.head_dim, pos0, m, scale, s)) ||
+          (e = gemm(L.wo, nullptr, c->pf_att, QD, nullptr, c->pf_x, nullptr, H, GEMM_RESID)) ||
+          (e = launch_rows_split(c->pf_x, m, H, L.ffn_norm, g.rms_eps, c->pf_xs, lo_of(c->pf_xs, H), s)) ||
+          (e = gemm(L.gate, L.up, c->pf_xs, H, nullptr, nullptr, c->pf_act, g.ffn, GEMM_SWIGLU)) ||
+          (e = gemm(L.down, nullptr, c->pf_act, g.ffn, nullptr, c->pf_x, nullptr, H, GEMM_RESID)))
         return e;
     }
   }

@@ -108,33 +108,43 @@ hipError_t launch_argmax(const float* x, size_t n, uint64_t* scratch, uint32_t* 
 // ---- prefill (prefill.hip) ----------------------------------------------------
 enum GemmMode : int { GEMM_STORE = 0, GEMM_RESID = 1, GEMM_SWIGLU = 2 };
 
-// C[P][N] = A'[P][K] . W[N][K]^T on MFMA; A' = A, or rmsnorm rows of A when
-// inv (per-row factor) and nw (gain) are given.  STORE: out = C (+ bias);
-// RESID: out += C; SWIGLU: out = silu(C(w)) * C(w2).
+// C[P][N] = A[P][K] . W[N][K]^T on bf16 MFMA.  A comes split into two bf16
+// planes, a_hi + a_lo (row stride K; launch_rows_split, the attention rows
+// and the SwiGLU epilogue write that form).  STORE: out = C (+ bias);
+// RESID: out += C; SWIGLU: silu(C(w)) * C(w2), split into the planes
+// o_hi / o_lo (row stride ldo).
 struct GemmArgs {
-  const float* a;       // [P][K] f32
-  const float* inv;     // optional [P]
-  const float* nw;      // optional [K]
-  const uint8_t* w;     // [N] rows of row_bytes raw blocks
-  const uint8_t* w2;    // SWIGLU: the up matrix
+  const uint16_t* a_hi;  // [P][K] bf16
+  const uint16_t* a_lo;  // [P][K] bf16
+  const uint8_t* w;      // [N] rows of row_bytes raw blocks
+  const uint8_t* w2;     // SWIGLU: the up matrix
   uint32_t type, row_bytes;
-  const float* bias;    // optional [N]
-  float* out;           // [P][ldo]
+  const float* bias;     // optional [N]
+  float* out;            // STORE / RESID: [P][ldo] f32
+  uint16_t* o_hi;        // SWIGLU: [P][ldo] bf16 planes
+  uint16_t* o_lo;
   uint32_t ldo, P, N, K;
 };
 hipError_t launch_gemm(const GemmArgs& g, GemmMode mode, hipStream_t s);
+// Raises the GEMM kernels' dynamic LDS limit (up to 120 KiB per block) on
+// the current device; once per device before the first launch_gemm.
+hipError_t gemm_prepare();
+// Rows of x [rows][cols] -- rmsnorm'd with gain nw (tensor.rs:164-185) when
+// nw is given -- split into the bf16 planes hi + lo that the GEMM reads.
+hipError_t launch_rows_split(const float* x, uint32_t rows, uint32_t cols, const float* nw, float eps, uint16_t* hi,
+                             uint16_t* lo, hipStream_t s);
 hipError_t launch_embed_rows(const uint8_t* table, uint32_t type, uint32_t hidden, uint32_t row_bytes,
                              const uint32_t* ids, uint32_t n, float* x, hipStream_t s);
-hipError_t launch_row_inv(const float* x, uint32_t rows, uint32_t cols, float eps, float* inv, hipStream_t s);
 // RoPE of n q rows (in place) and k rows (into the cache) at positions
 // pos0.., v rows into the cache.
 hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const float* rope_cs, float* k_cache,
                                float* v_cache, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                                uint32_t pos0, uint32_t n, hipStream_t s);
-// Causal attention of n query rows at positions pos0.. over the cache.
-hipError_t launch_attn_rows(const float* q, const float* k_cache, const float* v_cache, float* out, uint32_t n_heads,
-                            uint32_t n_kv_heads, uint32_t head_dim, uint32_t pos0, uint32_t n, float scale,
-                            hipStream_t s);
+// Causal attention of n query rows at positions pos0.. over the cache; the
+// output rows [n][n_heads * head_dim] as the GEMM's bf16 planes.
+hipError_t launch_attn_rows(const float* q, const float* k_cache, const float* v_cache, uint16_t* out_hi,
+                            uint16_t* out_lo, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t pos0,
+                            uint32_t n, float scale, hipStream_t s);
 // Argmax of the lm_head candidates into next_tok/tok, position += n.
 hipError_t launch_prefill_end(StepState* st, const uint64_t* best, uint32_t n_best, uint32_t n, hipStream_t s);
 

@@ -3,30 +3,33 @@
 // layer_forward_cached model.rs:444-478).
 //
 //  - k_embed_rows     embedding rows of the block's token ids
-//  - k_row_inv        1/sqrt(mean(x^2) + eps) per row (the rmsnorm factor)
-//  - k_gemm_q         C = A' . W^T with W in its raw GGUF blocks: each
-//                     k-step dequantizes a 64x32 weight tile (bit-exact f32,
-//                     the same formulas as the dequant kernel) and a 64x32
-//                     activation tile (rmsnorm applied on load) into LDS and
-//                     runs v_mfma_f32_32x32x2f32 on them; epilogues: store +
-//                     bias, residual add, SwiGLU of two weights
+//  - k_rows_split     rows of x, rmsnorm'd when a gain is given, split into
+//                     the bf16 planes x = hi + lo the GEMMs read
+//  - k_gemm_b3        C = A . W^T with W in its raw GGUF blocks: each
+//                     k-step dequantizes a weight tile (f32, the formulas
+//                     of the dequant kernel with fused products), splits it into
+//                     bf16 hi + lo in LDS beside the A planes, and runs
+//                     three v_mfma_f32_32x32x16_bf16 per tile pair (hi.hi,
+//                     hi.lo, lo.hi); epilogues: store + bias, residual add,
+//                     SwiGLU of two weights into split planes
 //  - k_rope_kv_rows   RoPE of q and k rows at their positions, KV append
 //  - k_attn_rows_mfma causal GQA attention of 32 query rows of one head over
 //                     the cache on v_mfma_f32_32x32x2f32 (S^T = K Q^T, then
 //                     O^T += V^T P^T), online softmax over 32-key tiles
 //
-// The MFMA operands are exact f32 (the dequantized weights are exact), so
-// the GEMM differs from the CPU path only by the order of its sums.
+// The split products carry 16+ significant bits per operand into f32
+// accumulators: the GEMM differs from the CPU path by the order of its
+// sums and a relative error below ~2^-15 per product.
+#include <stdlib.h>
+
+#include <type_traits>
+
 #include "formats.hpp"
 #include "kernels.hpp"
 
 namespace frn {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ float4 u4f_(uint4 v) {
-  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
-}
 
 // ---- embedding rows (model.rs:482-506) ----------------------------------------------
 __global__ void k_embed_rows(const uint8_t* __restrict__ table, uint32_t type, uint32_t hidden, uint32_t row_bytes,
@@ -46,28 +49,83 @@ hipError_t launch_embed_rows(const uint8_t* table, uint32_t type, uint32_t hidde
   return hipGetLastError();
 }
 
-// ---- rmsnorm factor per row (tensor.rs:164-185) -------------------------------------
-__global__ __launch_bounds__(256) void k_row_inv(const float* __restrict__ x, uint32_t cols, float eps,
-                                                 float* __restrict__ inv) {
-  __shared__ float red[4];
-  const float* row = x + (size_t)blockIdx.x * cols;
-  float ss = 0.f;
-  for (uint32_t i = threadIdx.x; i < cols; i += 256) ss += row[i] * row[i];
-  ss = group_reduce<64>(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  if (threadIdx.x == 0) inv[blockIdx.x] = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)cols + eps);
+// ---- bf16 split of operands ---------------------------------------------------------
+// x = hi + lo + e with hi = bf16(x) (to nearest even), lo = bf16(x - hi),
+// |e| <= 2^-16 |x| (bf16 keeps 8 significant bits).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// two values to a bf16 pair (value a in the low half), one v_cvt_pk_bf16_f32
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
+// a pair of values -> the pair of their bf16 hi and the pair of their lo
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = pk_bf16(a, b);
+  lo = pk_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
+}
+// 8 values -> 8 bf16 hi and 8 bf16 lo, value i in half i%2 of dword i/2
+// (the order of the MFMA operands)
+__device__ __forceinline__ void split8(const float (&y)[8], uint4& hi, uint4& lo) {
+  split2(y[0], y[1], hi.x, lo.x);
+  split2(y[2], y[3], hi.y, lo.y);
+  split2(y[4], y[5], hi.z, lo.z);
+  split2(y[6], y[7], hi.w, lo.w);
+}
+__device__ __forceinline__ void split1(float y, uint16_t& hi, uint16_t& lo) {
+  uint32_t h, l;
+  split2(y, 0.0f, h, l);
+  hi = (uint16_t)h;
+  lo = (uint16_t)l;
 }
 
-hipError_t launch_row_inv(const float* x, uint32_t rows, uint32_t cols, float eps, float* inv, hipStream_t s) {
-  hipLaunchKernelGGL(k_row_inv, dim3(rows), dim3(256), 0, s, x, cols, eps, inv);
+// One block per row: the rmsnorm factor 1/sqrt(mean(x^2) + eps) when nw is
+// given (tensor.rs:164-185: (x * inv) * w), then the split.  cols % 8 == 0.
+__global__ __launch_bounds__(256) void k_rows_split(const float* __restrict__ x, uint32_t cols,
+                                                    const float* __restrict__ nw, float eps, uint16_t* __restrict__ hi,
+                                                    uint16_t* __restrict__ lo) {
+  __shared__ float red[4];
+  const float* row = x + (size_t)blockIdx.x * cols;
+  float inv = 1.0f;
+  if (nw) {
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < cols; i += 256) ss += row[i] * row[i];
+    ss = group_reduce<64>(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)cols + eps);
+  }
+  for (uint32_t i = 8 * threadIdx.x; i < cols; i += 8 * 256) {
+    const float4 a = *(const float4*)(row + i), b = *(const float4*)(row + i + 4);
+    float y[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    if (nw) {
+      const float4 wa = *(const float4*)(nw + i), wb = *(const float4*)(nw + i + 4);
+      const float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = y[j] * inv * w[j];
+    }
+    uint4 h, l;
+    split8(y, h, l);
+    *(uint4*)(hi + (size_t)blockIdx.x * cols + i) = h;
+    *(uint4*)(lo + (size_t)blockIdx.x * cols + i) = l;
+  }
+}
+
+hipError_t launch_rows_split(const float* x, uint32_t rows, uint32_t cols, const float* nw, float eps, uint16_t* hi,
+                             uint16_t* lo, hipStream_t s) {
+  if (cols % 8) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rows_split, dim3(rows), dim3(256), 0, s, x, cols, nw, eps, hi, lo);
   return hipGetLastError();
 }
 
-// ---- quantized GEMM on MFMA ----------------------------------------------------
+// ---- weight tiles of the GEMM -------------------------------------------------------
 // Eight consecutive weights w[n][k .. k + 8) (k % 8 == 0, inside one 32-value
-// group) of a row at byte offset `row` (BUF_INVALID: zeros), bit-exact as
-// decode_elem.  Raw bytes are fetched by load(), decoded by decode().
+// group) of a row at byte offset `row` (BUF_INVALID: zeros): decode_elem's
+// formulas, the scale products fused (d*sc*q - dmin*m as one FMA; within
+// 2^-24 of the unfused value, far below the bf16 split that follows).
+// Raw bytes are fetched by load(), decoded by decode().
 template <uint32_t T>
 struct Deq8;
 
@@ -87,10 +145,12 @@ struct Deq8<T_Q4_K> {  // quant.rs:93-109
     q4k_scale_min_regs(hdr.y, hdr.z, hdr.w, (int)j, sc, m);
     const float dd = d * (float)sc, mm = dmin * (float)m;
     const uint32_t sh = (j & 1) ? 4 : 0;
+    // the 8 nibbles as bytes, then byte -> f32 conversions
+    const uint32_t n0 = (q.x >> sh) & 0x0F0F0F0Fu, n1 = (q.y >> sh) & 0x0F0F0F0Fu;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t b = ((i < 4 ? q.x : q.y) >> (8 * (i & 3))) & 0xFFu;
-      y[i] = dd * (float)((b >> sh) & 0x0Fu) - mm;
+    for (int i = 0; i < 4; ++i) {
+      y[i] = fmaf(dd, byte_f(n0, i), -mm);
+      y[4 + i] = fmaf(dd, byte_f(n1, i), -mm);
     }
   }
 };
@@ -121,11 +181,15 @@ struct Deq8<T_Q6_K> {  // quant.rs:114-133
     const uint32_t idx = k % 256, k6 = (idx % 128) / 32;
     const float dsc = f16_bits_to_f32(d & 0xFFFFu) * (float)(int8_t)(sc & 0xFFu);
     const uint32_t lsh = (k6 & 2) ? 4 : 0, hsh = 2 * k6;
+    // the 8 6-bit values as bytes (low nibble | 2 high bits << 4), then
+    // byte -> f32 and (v - 32) * d*sc as one FMA
+    const uint32_t v0 = ((ql.x >> lsh) & 0x0F0F0F0Fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
+    const uint32_t v1 = ((ql.y >> lsh) & 0x0F0F0F0Fu) | (((qh.y >> hsh) & 0x03030303u) << 4);
+    const float off = -32.0f * dsc;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t lo = ((i < 4 ? ql.x : ql.y) >> (8 * (i & 3) + lsh)) & 0x0Fu;
-      const uint32_t hi = ((i < 4 ? qh.x : qh.y) >> (8 * (i & 3) + hsh)) & 3u;
-      y[i] = dsc * (float)((int32_t)(lo | (hi << 4)) - 32);
+    for (int i = 0; i < 4; ++i) {
+      y[i] = fmaf(dsc, byte_f(v0, i), off);
+      y[4 + i] = fmaf(dsc, byte_f(v1, i), off);
     }
   }
 };
@@ -207,156 +271,306 @@ struct Deq8<T_F32> {
   }
 };
 
-// Block tile GM = 64 * MT rows of A (tokens) x 64 weight rows, k-steps of
-// 32; 4 waves, wave (wm, wn) owns the 32 * MT x 32 output sub-tile (wm, wn)
-// and runs 16 * MT v_mfma_f32_32x32x2f32 per k-step and weight matrix, so a
-// dequantized weight tile feeds MT times the MFMAs (the single-weight
-// GEMMs are bound by the dequantization at MT 1).  Lane l supplies
-// A[l%32][l/32] and W[l%32][l/32] of each k-pair; the accumulator's
-// register v of lane l is C[8(v/4) + 4(l/32) + v%4][l%32] (layouts checked
-// on gfx950).
-constexpr int GN = 64, GK = 32, GKP = GK + 1;  // LDS rows padded against bank conflicts
+// ---- the GEMM ---------------------------------------------------------------------
+// Block tile: (32 MT tokens) x (4 waves x 32 NJ weight rows) per weight
+// matrix, k-steps of 32.  The A planes of a k-step go through LDS (shared
+// by the 4 waves; double buffer, one barrier per k-step); each wave loads,
+// decodes and splits its own weight rows straight into MFMA operands, so
+// no weight value is decoded twice and the LDS carries only A.  Per k-step
+// a wave runs 2 x MT x NW x NJ x 3 v_mfma_f32_32x32x16_bf16 (hi.hi, hi.lo,
+// lo.hi; the lo.lo term is below 2^-14 of the product).  Lane l supplies
+// A[l%32][8(l/32) .. +8] and B[8(l/32) .. +8][l%32]; register v of lane l
+// is C[8(v/4) + 4(l/32) + v%4][l%32] (layouts checked on gfx950).  The raw
+// weight bytes of k-step t + 2 and the A planes of k-step t + 1 are in
+// flight while k-step t computes.  LDS rows of 32 bf16 are padded to 40
+// (80 bytes: the 16-byte reads of 16 consecutive rows hit distinct banks).
+constexpr int BKP = 40;
+template <int MT>
+__host__ __device__ constexpr uint32_t gemm_lds_bytes() {
+  return 2u * 2u * 32u * MT * BKP * 2u;  // 2 buffers x 2 planes x rows x padded row
+}
 
-template <uint32_t T, int MODE, int MT>
-__global__ __launch_bounds__(256) void k_gemm_q(GemmArgs g) {
-  constexpr int NW = MODE == GEMM_SWIGLU ? 2 : 1, GM = 64 * MT;
-  __shared__ float As[GM * GKP];
-  __shared__ float Ws[NW][GN * GKP];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave & 1, wn = wave >> 1;
-  const uint32_t r0 = blockIdx.y * GM, n0 = blockIdx.x * GN;
-  // tile loaders: thread t fills rows t/4 + 64 m (m < MT) of A and row t/4
-  // of W, k sub-range 8*(t%4)
-  const uint32_t lr = t / 4, lk = 8 * (t % 4);
-  const rsrc_t ra = make_rsrc(g.a, g.P * g.K * 4);
+template <uint32_t T, int MODE, int MT, int NJ>
+__global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
+  constexpr int NW = MODE == GEMM_SWIGLU ? 2 : 1, TM = 32 * MT, TN = 4 * 32 * NJ;
+  // A loaders: TM rows x 32 values x 2 planes per k-step = TM * 8 uint4;
+  // thread t takes rows t / 4 + 64 i (i < (TM + 63) / 64), 16-byte chunk t % 4
+  constexpr int AI = (TM + 63) / 64;
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds16[];
+  constexpr uint32_t A_PL = TM * BKP;
+  auto A = [&](int b, int p) { return lds16 + (2 * b + p) * A_PL; };
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, col = lane & 31, kh = 8 * (lane >> 5);
+  const uint32_t r0 = blockIdx.y * TM, n0 = blockIdx.x * TN + wave * 32 * NJ;
+  const uint32_t a_bytes = g.P * g.K * 2;
+  const rsrc_t rah = make_rsrc(g.a_hi, a_bytes), ral = make_rsrc(g.a_lo, a_bytes);
   const rsrc_t rw[2] = {make_rsrc(g.w, g.N * g.row_bytes), make_rsrc(NW == 2 ? g.w2 : g.w, g.N * g.row_bytes)};
-  const bool wrow = n0 + lr < g.N;
-  uint32_t a_off[MT];
-  float inv[MT];
+  const uint32_t nk = g.K / 32;
+  uint32_t a_off[AI];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    const uint32_t r = r0 + lr + 64 * m;
-    a_off[m] = r < g.P ? 4 * (r * g.K + lk) : BUF_INVALID;
-    inv[m] = (g.inv && r < g.P) ? g.inv[r] : 1.0f;
+  for (int i = 0; i < AI; ++i) {
+    const uint32_t r = t / 4 + 64 * i;
+    a_off[i] = r < TM && r0 + r < g.P ? 2 * ((r0 + r) * g.K + 8 * (t % 4)) : BUF_INVALID;
   }
-  const uint32_t w_off = wrow ? (n0 + lr) * g.row_bytes : BUF_INVALID;
-  const rsrc_t rn = make_rsrc(g.nw, g.nw ? g.K * 4 : 0);
+  // this lane's weight rows: n0 + 32 j + col
+  uint32_t w_off[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) w_off[j] = n0 + 32 * j + col < g.N ? (n0 + 32 * j + col) * g.row_bytes : BUF_INVALID;
 
-  float4 pa0[MT], pa1[MT], pn0, pn1;
-  Deq8<T> pw[NW];
-  auto fetch = [&](uint32_t k0) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      pa0[m] = u4f_(bl128(ra, a_off[m] == BUF_INVALID ? BUF_INVALID : a_off[m] + 4 * k0));
-      pa1[m] = u4f_(bl128(ra, a_off[m] == BUF_INVALID ? BUF_INVALID : a_off[m] + 4 * k0 + 16));
-    }
-    if (g.nw) {
-      pn0 = u4f_(bl128(rn, 4 * (k0 + lk)));
-      pn1 = u4f_(bl128(rn, 4 * (k0 + lk) + 16));
-    }
-#pragma unroll
-    for (int i = 0; i < NW; ++i) pw[i].load(rw[i], w_off, k0 + lk);
-  };
-  auto stage = [&](uint32_t k0) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      float av[8] = {pa0[m].x, pa0[m].y, pa0[m].z, pa0[m].w, pa1[m].x, pa1[m].y, pa1[m].z, pa1[m].w};
-      if (g.nw) {  // rmsnorm on load: (x * inv) * w (tensor.rs:181-183)
-        const float nv[8] = {pn0.x, pn0.y, pn0.z, pn0.w, pn1.x, pn1.y, pn1.z, pn1.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) av[i] = av[i] * inv[m] * nv[i];
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) As[(lr + 64 * m) * GKP + lk + i] = av[i];
-    }
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      float y[8];
-      pw[w].decode(k0 + lk, y);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) Ws[w][lr * GKP + lk + i] = y[i];
-    }
-  };
-
-  f32x16 acc[MT][NW];
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
+  // raw data of two k-steps in flight: A planes [set][i], weights [set][w][j][ks]
+  uint4 pah[2][AI], pal[2][AI];  // (one set used when ASETS == 1)
+  Deq8<T> pw[2][NW][NJ][2];
+  // Q4_K: per pair of k-steps (one 32-byte group of quants, sub-blocks 2G
+  // and 2G + 1 in its low and high nibbles) lane (row, half h) loads the
+  // group's bytes 16h .. 16h + 16 and the superblock header: two 16-byte
+  // loads per two k-steps instead of four 8- and 16-byte loads per k-step
+  // (the memory pipeline, not the matrix cores, bounds this GEMM).  The
+  // k order inside a k-step is permuted to match (MFMA half ks of lane
+  // half h takes values 16h + 8ks .. +8, in A as in W).
+  constexpr bool QK = T == T_Q4_K;
+  uint4 qhdr[2][NW][NJ], qraw[2][NW][NJ];
+  auto fetch_wq = [&](int s, uint32_t grp) {
+    const uint32_t sb = (grp / 4) * 144u, qo = sb + 16u + 32u * (grp % 4) + (uint32_t)(2 * kh);
 #pragma unroll
     for (int w = 0; w < NW; ++w)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[m][w][v] = 0.f;
-  const uint32_t nk = g.K / GK;
-  fetch(0);
-  stage(0);
-  __syncthreads();
-  // wave (wm, wn): A rows wm * 32 * MT + 32 m + lane % 32, W rows wn * 32 + lane % 32
-  const int ar = wm * 32 * MT + (lane & 31), wr = wn * 32 + (lane & 31), kh = lane >> 5;
-  for (uint32_t kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) fetch((kt + 1) * GK);
+      for (int j = 0; j < NJ; ++j) {
+        const bool ok = 2 * grp < nk && w_off[j] != BUF_INVALID;
+        qhdr[s][w][j] = bl128(rw[w], ok ? w_off[j] + sb : BUF_INVALID);
+        qraw[s][w][j] = bl128(rw[w], ok ? w_off[j] + qo : BUF_INVALID);
+      }
+  };
+  auto fetch_a = [&](int s, uint32_t kt) {
 #pragma unroll
-    for (int kk = 0; kk < GK; kk += 2) {
-      float wv[NW];
+    for (int i = 0; i < AI; ++i) {
+      const uint32_t o = a_off[i] == BUF_INVALID || kt >= nk ? BUF_INVALID : a_off[i] + 64 * kt;
+      pah[s][i] = bl128(rah, o);
+      pal[s][i] = bl128(ral, o);
+    }
+  };
+  auto put_a = [&](int s, int b) {
 #pragma unroll
-      for (int w = 0; w < NW; ++w) wv[w] = Ws[w][wr * GKP + kk + kh];
+    for (int i = 0; i < AI; ++i) {
+      const uint32_t r = t / 4 + 64 * i;
+      if (r < TM) {
+        *(uint4*)(A(b, 0) + r * BKP + 8 * (t % 4)) = pah[s][i];
+        *(uint4*)(A(b, 1) + r * BKP + 8 * (t % 4)) = pal[s][i];
+      }
+    }
+  };
+  auto fetch_w = [&](int s, uint32_t kt) {
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        const float a = As[(ar + 32 * m) * GKP + kk + kh];
+    for (int w = 0; w < NW; ++w)
 #pragma unroll
-        for (int w = 0; w < NW; ++w) acc[m][w] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, wv[w], acc[m][w], 0, 0, 0);
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          pw[s][w][j][ks].load(rw[w], kt >= nk ? BUF_INVALID : w_off[j], 32 * kt + 16 * ks + kh);
+  };
+
+  f32x16 acc[MT][NW][NJ];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][w][j][v] = 0.f;
+
+  // k-step kt: LDS buffer kt & 1, weight register set kt & 1.  Two k-steps
+  // per trip keep every buffer and set index a constant (a register array
+  // indexed at run time would live in scratch memory).
+  // One k-step kt (LDS buffer and register sets b = kt & 1): all of its A
+  // operands are read from LDS up front (a read just before its MFMA would
+  // stall the matrix pipe on the LDS latency), the weight operands of the
+  // first half are decoded, then the MFMAs run with the accumulators
+  // alternating (independent MFMAs back to back) while the second half's
+  // weights are decoded.  Then: weights of k-step kt + 2 into set b, the A
+  // planes of k-step kt + 1 (fetched a step earlier) into LDS buffer b ^ 1,
+  // and A of k-step kt + 3 into the set they came from, so every load has
+  // two k-steps of compute to arrive.
+  // SwiGLU's MT 4 tile keeps one set of A registers (fetched a k-step
+  // ahead) so that two waves per SIMD still fit; the others keep two
+  constexpr int ASETS = NW == 2 && MT == 4 ? 1 : 2;
+  auto step = [&](auto bc, auto sc_, auto hc, uint32_t kt) {
+    constexpr int b = decltype(bc)::value, S = decltype(sc_)::value, H = decltype(hc)::value;
+    if constexpr (ASETS == 1) {
+      if (kt + 1 < nk) fetch_a(0, kt + 1);
+    }
+    bf16x8 ah[2][MT], al[2][MT], bh[2][NW][NJ], bl[2][NW][NJ];
+    auto read_a = [&](int ks) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const uint32_t ko = QK ? 2 * kh + 8 * ks : 16 * ks + kh;
+        ah[ks][i] = *(const bf16x8*)(A(b, 0) + (32 * i + col) * BKP + ko);
+        al[ks][i] = *(const bf16x8*)(A(b, 1) + (32 * i + col) * BKP + ko);
+      }
+    };
+    // both halves' A operands up front when the registers allow (one
+    // weight matrix); with two (SwiGLU) the second half's are read once
+    // the first half's MFMAs are issued, so they reuse its registers
+    constexpr bool A_EARLY = NW == 1 || MT <= 2;
+    read_a(0);
+    if constexpr (A_EARLY) read_a(1);
+    auto decode = [&](int ks) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          float y[8];
+          if constexpr (QK) {  // quant.rs:93-109, sub-block kt % 8
+            const uint4 hd = qhdr[S][w][j], q = qraw[S][w][j];
+            const float d = f16_bits_to_f32(hd.x & 0xFFFFu), dmin = f16_bits_to_f32(hd.x >> 16);
+            uint32_t sc, m;
+            q4k_scale_min_regs(hd.y, hd.z, hd.w, (int)(kt % 8), sc, m);
+            const float dd = d * (float)sc, mm = dmin * (float)m;
+            const uint32_t n0 = ((ks ? q.z : q.x) >> (4 * H)) & 0x0F0F0F0Fu;
+            const uint32_t n1 = ((ks ? q.w : q.y) >> (4 * H)) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              y[i] = fmaf(dd, byte_f(n0, i), -mm);
+              y[4 + i] = fmaf(dd, byte_f(n1, i), -mm);
+            }
+          } else {
+            pw[b][w][j][ks].decode(32 * kt + 16 * ks + kh, y);
+          }
+          uint4 hi, lo;
+          split8(y, hi, lo);
+          bh[ks][w][j] = __builtin_bit_cast(bf16x8, hi);
+          bl[ks][w][j] = __builtin_bit_cast(bf16x8, lo);
+        }
+    };
+    auto mma = [&](int ks) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+            acc[i][w][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[ks][i], bh[ks][w][j], acc[i][w][j], 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+            acc[i][w][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[ks][i], bl[ks][w][j], acc[i][w][j], 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+            acc[i][w][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[ks][i], bh[ks][w][j], acc[i][w][j], 0, 0, 0);
+        }
+    };
+    decode(0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0);
+    if constexpr (!A_EARLY) {
+      __builtin_amdgcn_sched_barrier(0);
+      read_a(1);
+    }
+    decode(1);
+    mma(1);
+    // weights two k-steps (Q4_K: two groups) ahead; past the end: no memory access
+    if constexpr (QK) {
+      if (H == 1) fetch_wq(S, (kt + 3) / 2);
+    } else {
+      fetch_w(b, kt + 2);
+    }
+    if (kt + 1 < nk) {
+      if constexpr (ASETS == 1) {
+        put_a(0, b ^ 1);
+      } else {
+        put_a(b ^ 1, b ^ 1);
+        fetch_a(b ^ 1, kt + 3);
       }
     }
     __syncthreads();
-    if (kt + 1 < nk) {
-      stage((kt + 1) * GK);
-      __syncthreads();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  fetch_a(0, 0);
+  if constexpr (ASETS == 2) fetch_a(1, 1);
+  if constexpr (QK) {
+    fetch_wq(0, 0);
+    fetch_wq(1, 1);
+  } else {
+    fetch_w(0, 0);
+    fetch_w(1, 1);
+  }
+  put_a(0, 0);
+  if constexpr (ASETS == 2) fetch_a(0, 2);
+  __syncthreads();
+  if constexpr (QK) {
+    // four k-steps (two groups) per trip; Q4_K rows hold a multiple of 256
+    // values, so nk % 8 == 0
+    for (uint32_t kt = 0; kt < nk; kt += 4) {
+      step(I0{}, I0{}, I0{}, kt);
+      step(I1{}, I0{}, I1{}, kt + 1);
+      step(I0{}, I1{}, I0{}, kt + 2);
+      step(I1{}, I1{}, I1{}, kt + 3);
+    }
+  } else {
+    for (uint32_t kt = 0; kt < nk; kt += 2) {
+      step(I0{}, I0{}, I0{}, kt);
+      if (kt + 1 < nk) step(I1{}, I0{}, I0{}, kt + 1);
     }
   }
   // epilogue: register v of lane l is C[8(v/4) + 4(l/32) + v%4][l%32]
-  const uint32_t n = n0 + wn * 32 + (lane & 31);
-  if (n >= g.N) return;
-  const float bias = (MODE == GEMM_STORE && g.bias) ? g.bias[n] : 0.f;
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
+  for (int j = 0; j < NJ; ++j) {
+    const uint32_t n = n0 + 32 * j + col;
+    if (n >= g.N) continue;
+    const float bias = (MODE == GEMM_STORE && g.bias) ? g.bias[n] : 0.f;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const uint32_t r = r0 + wm * 32 * MT + 32 * m + 8 * (v / 4) + 4 * (lane >> 5) + (v & 3);
-      if (r >= g.P) continue;
-      float* o = g.out + (size_t)r * g.ldo + n;
-      if (MODE == GEMM_STORE) *o = g.bias ? acc[m][0][v] + bias : acc[m][0][v];  // model.rs:179-183
-      if (MODE == GEMM_RESID) *o = *o + acc[m][0][v];                            // tensor.rs:232
-      if (MODE == GEMM_SWIGLU) {                                                 // tensor.rs:224
-        const float gg = acc[m][0][v];
-        *o = gg / (1.0f + expf(-gg)) * acc[m][NW - 1][v];
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const uint32_t r = r0 + 32 * i + 8 * (v / 4) + 4 * (lane >> 5) + (v & 3);
+        if (r >= g.P) continue;
+        const size_t o = (size_t)r * g.ldo + n;
+        if (MODE == GEMM_STORE) g.out[o] = g.bias ? acc[i][0][j][v] + bias : acc[i][0][j][v];  // model.rs:179-183
+        if (MODE == GEMM_RESID) g.out[o] = g.out[o] + acc[i][0][j][v];                         // tensor.rs:232
+        if (MODE == GEMM_SWIGLU) {                                                             // tensor.rs:224
+          const float gg = acc[i][0][j][v];
+          split1(gg / (1.0f + expf(-gg)) * acc[i][NW - 1][j][v], g.o_hi[o], g.o_lo[o]);
+        }
       }
-    }
+  }
 }
 
-// Row blocks of 128 (MT 2) once the prompt block has the rows to keep the
-// grid full; 64 below.  Measured: 7B 2048-token prefill 8,090 -> 8,185
-// tokens/s, 1.5B 4096-token 34,790 -> 35,480 (the GEMMs are not bound by
-// the dequantization alone).
-template <int MODE, int MT>
-static hipError_t gemm_go_mt(const GemmArgs& g, hipStream_t s) {
-  dim3 grid((g.N + GN - 1) / GN, (g.P + 64 * MT - 1) / (64 * MT));
+template <int MODE, int MT, int NJ>
+static hipError_t gemm_go_b3(const GemmArgs& g, hipStream_t s) {
+  dim3 grid((g.N + 128 * NJ - 1) / (128 * NJ), (g.P + 32 * MT - 1) / (32 * MT));
+  constexpr uint32_t lds = gemm_lds_bytes<MT>();
+  if constexpr (MODE == GEMM_SWIGLU && MT == 4) {  // Q4_K only (gemm_go)
+    if (g.type != T_Q4_K) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_gemm_b3<T_Q4_K, MODE, MT, NJ>), grid, dim3(256), lds, s, g);
+    return hipGetLastError();
+  }
   switch (g.type) {
-    case T_Q4_K: hipLaunchKernelGGL((k_gemm_q<T_Q4_K, MODE, MT>), grid, dim3(256), 0, s, g); break;
-    case T_Q6_K: hipLaunchKernelGGL((k_gemm_q<T_Q6_K, MODE, MT>), grid, dim3(256), 0, s, g); break;
-    case T_Q8_0: hipLaunchKernelGGL((k_gemm_q<T_Q8_0, MODE, MT>), grid, dim3(256), 0, s, g); break;
-    case T_Q5_0: hipLaunchKernelGGL((k_gemm_q<T_Q5_0, MODE, MT>), grid, dim3(256), 0, s, g); break;
-    case T_F32: hipLaunchKernelGGL((k_gemm_q<T_F32, MODE, MT>), grid, dim3(256), 0, s, g); break;
-    case T_F16: hipLaunchKernelGGL((k_gemm_q<T_F16, MODE, MT>), grid, dim3(256), 0, s, g); break;
+    case T_Q4_K: hipLaunchKernelGGL((k_gemm_b3<T_Q4_K, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
+    case T_Q6_K: hipLaunchKernelGGL((k_gemm_b3<T_Q6_K, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
+    case T_Q8_0: hipLaunchKernelGGL((k_gemm_b3<T_Q8_0, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
+    case T_Q5_0: hipLaunchKernelGGL((k_gemm_b3<T_Q5_0, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
+    case T_F32: hipLaunchKernelGGL((k_gemm_b3<T_F32, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
+    case T_F16: hipLaunchKernelGGL((k_gemm_b3<T_F16, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
+// Tiles of 128 weight rows per matrix by 32 MT tokens: MT 4 (128 tokens)
+// above 64 rows, MT 2 above 32, MT 1 below.  SwiGLU's two matrices take MT
+// 4 only in Q4_K, whose weight registers leave room for it at two waves
+// per SIMD (the other formats' would spill).
 template <int MODE>
 static hipError_t gemm_go(const GemmArgs& g, hipStream_t s) {
-  return g.P >= 512 ? gemm_go_mt<MODE, 2>(g, s) : gemm_go_mt<MODE, 1>(g, s);
+  if (g.P > 64 && (MODE != GEMM_SWIGLU || g.type == T_Q4_K)) return gemm_go_b3<MODE, 4, 1>(g, s);
+  if (g.P > 32) return gemm_go_b3<MODE, 2, 1>(g, s);
+  return gemm_go_b3<MODE, 1, 1>(g, s);
 }
 
+hipError_t gemm_prepare() { return hipSuccess; }
+
 hipError_t launch_gemm(const GemmArgs& g, GemmMode mode, hipStream_t s) {
-  if (g.K % GK || g.P == 0 || g.N == 0) return hipErrorInvalidValue;
-  if ((uint64_t)g.N * g.row_bytes >= BUF_INVALID || (uint64_t)g.P * g.K * 4 >= BUF_INVALID) return hipErrorInvalidValue;
+  if (g.K % 32 || g.P == 0 || g.N == 0) return hipErrorInvalidValue;
+  if ((uint64_t)g.N * g.row_bytes >= BUF_INVALID || (uint64_t)g.P * g.K * 2 >= BUF_INVALID) return hipErrorInvalidValue;
+  if (mode == GEMM_SWIGLU ? (!g.o_hi || !g.o_lo) : !g.out) return hipErrorInvalidValue;
   switch (mode) {
     case GEMM_STORE: return gemm_go<GEMM_STORE>(g, s);
     case GEMM_RESID: return gemm_go<GEMM_RESID>(g, s);
@@ -414,7 +628,8 @@ hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const f
 // CPU path (model.rs:371-438).
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_rows_mfma(const float* __restrict__ q, const float* __restrict__ kc,
-                                                        const float* __restrict__ vc, float* __restrict__ out,
+                                                        const float* __restrict__ vc, uint16_t* __restrict__ out_hi,
+                                                        uint16_t* __restrict__ out_lo,
                                                         uint32_t nh, uint32_t nkv, uint32_t pos0, uint32_t n,
                                                         float scale) {
   constexpr int NW = 4, DPL = HD / 32, NQ = HD / 8, OLD = HD + 1;  // O rows padded against bank conflicts
@@ -527,19 +742,31 @@ __global__ __launch_bounds__(256) void k_attn_rows_mfma(const float* __restrict_
   for (int ww = 0; ww < NW; ++ww) Mq = fmaxf(Mq, mls[ww][0][qq]);
 #pragma unroll
   for (int ww = 0; ww < NW; ++ww) L += weight(ww, qq, Mq) * mls[ww][1][qq];
-  float* orow = out + (size_t)(q0 + qq) * qd + h * HD + d0;
+  // the o-proj GEMM's operand form: bf16 hi + lo planes
+  const size_t ob = (size_t)(q0 + qq) * qd + h * HD + d0;
 #pragma unroll
-  for (int d = 0; d < HD / 8; ++d) orow[d] = os[qq * OLD + d0 + d] / L;
+  for (int d = 0; d < HD / 8; d += 8) {
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = os[qq * OLD + d0 + d + i] / L;
+    uint4 hi, lo;
+    split8(y, hi, lo);
+    *(uint4*)(out_hi + ob + d) = hi;
+    *(uint4*)(out_lo + ob + d) = lo;
+  }
 }
 
-hipError_t launch_attn_rows(const float* q, const float* kc, const float* vc, float* out, uint32_t nh, uint32_t nkv,
-                            uint32_t hd, uint32_t pos0, uint32_t n, float scale, hipStream_t s) {
+hipError_t launch_attn_rows(const float* q, const float* kc, const float* vc, uint16_t* out_hi, uint16_t* out_lo,
+                            uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t pos0, uint32_t n, float scale,
+                            hipStream_t s) {
   if (n == 0 || nkv == 0 || nh % nkv) return hipErrorInvalidValue;
   dim3 grid((n + 31) / 32, nh);
   if (hd == 128)
-    hipLaunchKernelGGL((k_attn_rows_mfma<128>), grid, dim3(256), 0, s, q, kc, vc, out, nh, nkv, pos0, n, scale);
+    hipLaunchKernelGGL((k_attn_rows_mfma<128>), grid, dim3(256), 0, s, q, kc, vc, out_hi, out_lo, nh, nkv, pos0, n,
+                       scale);
   else if (hd == 64)
-    hipLaunchKernelGGL((k_attn_rows_mfma<64>), grid, dim3(256), 0, s, q, kc, vc, out, nh, nkv, pos0, n, scale);
+    hipLaunchKernelGGL((k_attn_rows_mfma<64>), grid, dim3(256), 0, s, q, kc, vc, out_hi, out_lo, nh, nkv, pos0, n,
+                       scale);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
