@@ -339,6 +339,41 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
         qraw[s][w][j] = bl128(rw[w], ok ? w_off[j] + qo : BUF_INVALID);
       }
   };
+  // Q6_K: per half superblock (four k-steps, quarters k6 of 32 values) lane
+  // (row, half h) loads ql bytes 32p + 16h .. +16 (p = k6 & 1: low
+  // nibbles for k6 < 2, high above), qh bytes 16h .. +16 (2 bits per k6),
+  // the half's 8 scale bytes and d; 20-byte loads from the dword below,
+  // realigned on use (superblocks are 2-byte aligned).  Same permuted k
+  // order as Q4_K.
+  constexpr bool Q6 = T == T_Q6_K;
+  struct Raw20 {
+    uint4 a;
+    uint32_t x;
+  };
+  Raw20 q6l[Q6 ? 2 : 1][NW][NJ][2], q6h[Q6 ? 2 : 1][NW][NJ];
+  uint4 q6s[Q6 ? 2 : 1][NW][NJ];
+  uint32_t q6d[Q6 ? 2 : 1][NW][NJ];
+  auto fetch_w6 = [&](int s, uint32_t half) {
+    const uint32_t sbo = (half / 2) * 210u, hh = half % 2;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const bool ok = 4 * half < nk && w_off[j] != BUF_INVALID;
+        const uint32_t base = ok ? w_off[j] + sbo : BUF_INVALID, al = base & ~3u;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const uint32_t o = al + 64u * hh + 32u * p + (uint32_t)(2 * kh);
+          q6l[s][w][j][p].a = bl128(rw[w], o);
+          q6l[s][w][j][p].x = bl32(rw[w], o + 16u);
+        }
+        const uint32_t oh = al + 128u + 32u * hh + (uint32_t)(2 * kh);
+        q6h[s][w][j].a = bl128(rw[w], oh);
+        q6h[s][w][j].x = bl32(rw[w], oh + 16u);
+        q6s[s][w][j] = bl128(rw[w], al + 192u + 8u * hh);
+        q6d[s][w][j] = bl32(rw[w], al + 208u);
+      }
+  };
   auto fetch_a = [&](int s, uint32_t kt) {
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
@@ -392,8 +427,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   // SwiGLU's MT 4 tile keeps one set of A registers (fetched a k-step
   // ahead) so that two waves per SIMD still fit; the others keep two
   constexpr int ASETS = NW == 2 && MT == 4 ? 1 : 2;
-  auto step = [&](auto bc, auto sc_, auto hc, uint32_t kt) {
-    constexpr int b = decltype(bc)::value, S = decltype(sc_)::value, H = decltype(hc)::value;
+  // pc: the k-step's position in the loop trip (a constant): LDS buffer
+  // pc % 2; Q4_K register set pc / 2 and nibble half pc % 2; Q6_K register
+  // set pc / 4 and quarter pc % 4
+  auto step = [&](auto pcc, uint32_t kt) {
+    constexpr int pc = decltype(pcc)::value, b = pc % 2, S = Q6 ? pc / 4 : pc / 2, H = pc % 2, K6 = pc % 4;
     if constexpr (ASETS == 1) {
       if (kt + 1 < nk) fetch_a(0, kt + 1);
     }
@@ -401,7 +439,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
     auto read_a = [&](int ks) {
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
-        const uint32_t ko = QK ? 2 * kh + 8 * ks : 16 * ks + kh;
+        const uint32_t ko = (QK || Q6) ? 2 * kh + 8 * ks : 16 * ks + kh;
         ah[ks][i] = *(const bf16x8*)(A(b, 0) + (32 * i + col) * BKP + ko);
         al[ks][i] = *(const bf16x8*)(A(b, 1) + (32 * i + col) * BKP + ko);
       }
@@ -430,6 +468,24 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
             for (int i = 0; i < 4; ++i) {
               y[i] = fmaf(dd, byte_f(n0, i), -mm);
               y[4 + i] = fmaf(dd, byte_f(n1, i), -mm);
+            }
+          } else if constexpr (Q6) {  // quant.rs:114-133, quarter K6 of half (kt / 4) % 2
+            const uint32_t sh = (w_off[j] + (kt / 8) * 210u) & 3u;
+            uint32_t lo4[4], hi4[4];
+            realign16(q6l[S][w][j][K6 & 1].a, q6l[S][w][j][K6 & 1].x, sh, lo4);
+            realign16(q6h[S][w][j].a, q6h[S][w][j].x, sh, hi4);
+            const uint4 sw = q6s[S][w][j];
+            const uint32_t sb = sh + 2 * K6 + (kh >> 3), sd = sb >> 2;  // scale byte of this half lane
+            const uint32_t sword = sd == 0 ? sw.x : sd == 1 ? sw.y : sd == 2 ? sw.z : sw.w;
+            const float dsc = f16_bits_to_f32(q6d[S][w][j] >> (8 * sh) & 0xFFFFu) *
+                              (float)(int8_t)((sword >> (8 * (sb & 3))) & 0xFFu);
+            const float off = -32.0f * dsc;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const uint32_t nib = ((K6 & 2) ? lo4[2 * ks + e] >> 4 : lo4[2 * ks + e]) & 0x0F0F0F0Fu;
+              const uint32_t v = nib | (((hi4[2 * ks + e] >> (2 * K6)) & 0x03030303u) << 4);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) y[4 * e + i] = fmaf(dsc, byte_f(v, i), off);
             }
           } else {
             pw[b][w][j][ks].decode(32 * kt + 16 * ks + kh, y);
@@ -468,6 +524,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
     // weights two k-steps (Q4_K: two groups) ahead; past the end: no memory access
     if constexpr (QK) {
       if (H == 1) fetch_wq(S, (kt + 3) / 2);
+    } else if constexpr (Q6) {
+      if (K6 == 3) fetch_w6(S, kt / 4 + 2);
     } else {
       fetch_w(b, kt + 2);
     }
@@ -488,6 +546,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   if constexpr (QK) {
     fetch_wq(0, 0);
     fetch_wq(1, 1);
+  } else if constexpr (Q6) {
+    fetch_w6(0, 0);
+    fetch_w6(1, 1);
   } else {
     fetch_w(0, 0);
     fetch_w(1, 1);
@@ -496,18 +557,30 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   if constexpr (ASETS == 2) fetch_a(0, 2);
   __syncthreads();
   if constexpr (QK) {
-    // four k-steps (two groups) per trip; Q4_K rows hold a multiple of 256
-    // values, so nk % 8 == 0
+    // four k-steps (two groups) per trip; K-quant rows hold a multiple of
+    // 256 values, so nk % 8 == 0
     for (uint32_t kt = 0; kt < nk; kt += 4) {
-      step(I0{}, I0{}, I0{}, kt);
-      step(I1{}, I0{}, I1{}, kt + 1);
-      step(I0{}, I1{}, I0{}, kt + 2);
-      step(I1{}, I1{}, I1{}, kt + 3);
+      step(I0{}, kt);
+      step(I1{}, kt + 1);
+      step(std::integral_constant<int, 2>{}, kt + 2);
+      step(std::integral_constant<int, 3>{}, kt + 3);
+    }
+  } else if constexpr (Q6) {
+    // eight k-steps (a superblock: its two halves) per trip
+    for (uint32_t kt = 0; kt < nk; kt += 8) {
+      step(std::integral_constant<int, 0>{}, kt);
+      step(std::integral_constant<int, 1>{}, kt + 1);
+      step(std::integral_constant<int, 2>{}, kt + 2);
+      step(std::integral_constant<int, 3>{}, kt + 3);
+      step(std::integral_constant<int, 4>{}, kt + 4);
+      step(std::integral_constant<int, 5>{}, kt + 5);
+      step(std::integral_constant<int, 6>{}, kt + 6);
+      step(std::integral_constant<int, 7>{}, kt + 7);
     }
   } else {
     for (uint32_t kt = 0; kt < nk; kt += 2) {
-      step(I0{}, I0{}, I0{}, kt);
-      if (kt + 1 < nk) step(I1{}, I0{}, I0{}, kt + 1);
+      step(I0{}, kt);
+      if (kt + 1 < nk) step(I1{}, kt + 1);
     }
   }
   // epilogue: register v of lane l is C[8(v/4) + 4(l/32) + v%4][l%32]
@@ -534,6 +607,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
 }
 
 template <int MODE, int MT, int NJ>
+static hipError_t gemm_go_types(const GemmArgs& g, dim3 grid, uint32_t lds, hipStream_t s);
+
+template <int MODE, int MT, int NJ>
 static hipError_t gemm_go_b3(const GemmArgs& g, hipStream_t s) {
   dim3 grid((g.N + 128 * NJ - 1) / (128 * NJ), (g.P + 32 * MT - 1) / (32 * MT));
   constexpr uint32_t lds = gemm_lds_bytes<MT>();
@@ -541,7 +617,13 @@ static hipError_t gemm_go_b3(const GemmArgs& g, hipStream_t s) {
     if (g.type != T_Q4_K) return hipErrorInvalidValue;
     hipLaunchKernelGGL((k_gemm_b3<T_Q4_K, MODE, MT, NJ>), grid, dim3(256), lds, s, g);
     return hipGetLastError();
+  } else {
+    return gemm_go_types<MODE, MT, NJ>(g, grid, lds, s);
   }
+}
+
+template <int MODE, int MT, int NJ>
+static hipError_t gemm_go_types(const GemmArgs& g, dim3 grid, uint32_t lds, hipStream_t s) {
   switch (g.type) {
     case T_Q4_K: hipLaunchKernelGGL((k_gemm_b3<T_Q4_K, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
     case T_Q6_K: hipLaunchKernelGGL((k_gemm_b3<T_Q6_K, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;

@@ -124,6 +124,35 @@ def test_full_model_greedy_ids_and_logits(hip, tmpdir_models, preset, n_prompt):
     os.remove(path)
 
 
+@pytest.mark.parametrize("mix", ["q4_k_m", "q6_k", "q8_0"])
+def test_prefill_block_sizes(hip, tmpdir_models, mix):
+    """Prompt lengths that run each prefill GEMM tile height (32, 64 and 128
+    token rows, full and partial), for the formats
+    with their own weight loaders (Q4_K, Q6_K) and the generic one (Q8_0):
+    the last-position logits and the KV cache against the oracle."""
+    spec = dict(n_layers=2, n_heads=4, n_kv_heads=2, hidden=512, ffn=768, vocab=1000, tied=1,
+                mix={"q4_k_m": fa.MIX_Q4_K_M, "q6_k": fa.MIX_ALL_Q6_K, "q8_0": fa.MIX_ALL_Q8_0}[mix],
+                embd_type=fa.Q6_K if mix != "q8_0" else fa.Q8_0, output_type=fa.Q8_0)
+    path = os.path.join(tmpdir_models, "blocks-%s.gguf" % mix)
+    fa.synth_write(path, seed=53, **spec)
+    for n in (2, 31, 40, 64, 100, 257):
+        prompt = np.random.default_rng(n).integers(0, spec["vocab"], n).astype(np.uint32)
+        print("%s prompt %d" % (mix, n), flush=True)
+        ref = orc.Model(path)
+        ref.new_cache(300)
+        ref_logits = ref.forward_cached(prompt)
+        m = fa.Model(path, max_ctx=300)
+        nxt = m.prefill(prompt)
+        assert np.max(np.abs(m.logits() - ref_logits)) <= LOGIT_TOL, n
+        assert nxt == orc.argmax(ref_logits), n
+        got_k = m.cache_read(1, 0, n)
+        want_k = ref.cache_read(1, False, n)
+        assert np.max(np.abs(got_k - want_k)) <= 1e-3 * max(1.0, float(np.max(np.abs(want_k)))), n
+        m.close()
+        ref.close()
+    os.remove(path)
+
+
 def test_7b_greedy_ids_and_logits(hip, tmpdir_models):
     """Qwen2-7B shape (hidden 3584, FFN 18944, 7 query heads per kv head,
     untied Q6_K lm_head, Q4_K embedding): a 16-token prompt keeps the
