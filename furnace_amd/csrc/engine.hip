@@ -830,13 +830,42 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
       ga.K = K;
       return launch_gemm(ga, mode, s);
     };
+    // q, k and v: one launch for the matrices that share a format
+    auto qkv = [&](const LayerPtrs& L) {
+      const DevTensor* w[3] = {L.wq, L.wk, L.wv};
+      const float* b[3] = {L.bq, L.bk, L.bv};
+      float* o[3] = {c->pf_q, c->pf_k, c->pf_v};
+      const uint32_t ld[3] = {QD, KVD, KVD};
+      bool done[3] = {false, false, false};
+      for (int i = 0; i < 3; ++i) {
+        if (done[i]) continue;
+        GemmArgs ga{};
+        ga.a_hi = c->pf_xs;
+        ga.a_lo = lo_of(c->pf_xs, H);
+        ga.w = w[i]->ptr;
+        ga.type = w[i]->type;
+        ga.row_bytes = (uint32_t)type_row_bytes(w[i]->type, w[i]->in);
+        ga.bias = b[i];
+        ga.out = o[i];
+        ga.ldo = ld[i];
+        ga.P = m;
+        ga.N = (uint32_t)w[i]->out;
+        ga.K = H;
+        done[i] = true;
+        for (int k = i + 1; k < 3; ++k)
+          if (!done[k] && w[k]->type == w[i]->type) {
+            ga.more[ga.n_more++] = GemmArgs::More{w[k]->ptr, b[k], o[k], (uint32_t)w[k]->out, ld[k]};
+            done[k] = true;
+          }
+        if (hipError_t r = launch_gemm(ga, GEMM_STORE, s)) return r;
+      }
+      return hipSuccess;
+    };
     for (uint32_t l = 0; l < g.n_layers; ++l) {
       const LayerPtrs& L = c->layers[l];
       const size_t lo = (size_t)l * g.max_ctx * KVD;
       if ((e = launch_rows_split(c->pf_x, m, H, L.attn_norm, g.rms_eps, c->pf_xs, lo_of(c->pf_xs, H), s)) ||
-          (e = gemm(L.wq, nullptr, c->pf_xs, H, L.bq, c->pf_q, nullptr, QD, GEMM_STORE)) ||
-          (e = gemm(L.wk, nullptr, c->pf_xs, H, L.bk, c->pf_k, nullptr, KVD, GEMM_STORE)) ||
-          (e = gemm(L.wv, nullptr, c->pf_xs, H, L.bv, c->pf_v, nullptr, KVD, GEMM_STORE)) ||
+          (e = qkv(L)) ||
           (e = launch_rope_kv_rows(c->pf_q, c->pf_k, c->pf_v, c->rope, c->kcache + lo, c->vcache + lo, g.n_heads,
                                    g.n_kv_heads, g.head_dim, pos0, m, s)) ||
           (e = launch_attn_rows(c->pf_q, c->kcache + lo, c->vcache + lo, c->pf_att, lo_of(c->pf_att, QD), g.n_heads,

@@ -124,6 +124,16 @@ struct GemmArgs {
   uint16_t* o_hi;        // SWIGLU: [P][ldo] bf16 planes
   uint16_t* o_lo;
   uint32_t ldo, P, N, K;
+  // STORE: up to two more weight matrices of the same type and K on the
+  // same A (a layer's q, k and v), with their own bias, output and ldo; one
+  // launch, their tiles after segment 0's
+  uint32_t n_more;
+  struct More {
+    const uint8_t* w;
+    const float* bias;
+    float* out;
+    uint32_t N, ldo;
+  } more[2];
 };
 hipError_t launch_gemm(const GemmArgs& g, GemmMode mode, hipStream_t s);
 // Raises the GEMM kernels' dynamic LDS limit (up to 120 KiB per block) on

@@ -300,10 +300,27 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   constexpr uint32_t A_PL = TM * BKP;
   auto A = [&](int b, int p) { return lds16 + (2 * b + p) * A_PL; };
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, col = lane & 31, kh = 8 * (lane >> 5);
-  const uint32_t r0 = blockIdx.y * TM, n0 = blockIdx.x * TN + wave * 32 * NJ;
+  // the block's weight matrix (segment) and its tile within it
+  const uint8_t* sw = g.w;
+  const float* sbias = g.bias;
+  float* sout = g.out;
+  uint32_t sN = g.N, sldo = g.ldo, tile = blockIdx.x;
+  if (MODE == GEMM_STORE) {
+    for (uint32_t i = 0; i < g.n_more; ++i) {
+      const uint32_t tiles = (sN + TN - 1) / TN;
+      if (tile < tiles) break;
+      tile -= tiles;
+      sw = g.more[i].w;
+      sbias = g.more[i].bias;
+      sout = g.more[i].out;
+      sN = g.more[i].N;
+      sldo = g.more[i].ldo;
+    }
+  }
+  const uint32_t r0 = blockIdx.y * TM, n0 = tile * TN + wave * 32 * NJ;
   const uint32_t a_bytes = g.P * g.K * 2;
   const rsrc_t rah = make_rsrc(g.a_hi, a_bytes), ral = make_rsrc(g.a_lo, a_bytes);
-  const rsrc_t rw[2] = {make_rsrc(g.w, g.N * g.row_bytes), make_rsrc(NW == 2 ? g.w2 : g.w, g.N * g.row_bytes)};
+  const rsrc_t rw[2] = {make_rsrc(sw, sN * g.row_bytes), make_rsrc(NW == 2 ? g.w2 : sw, sN * g.row_bytes)};
   const uint32_t nk = g.K / 32;
   uint32_t a_off[AI];
 #pragma unroll
@@ -314,7 +331,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   // this lane's weight rows: n0 + 32 j + col
   uint32_t w_off[NJ];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) w_off[j] = n0 + 32 * j + col < g.N ? (n0 + 32 * j + col) * g.row_bytes : BUF_INVALID;
+  for (int j = 0; j < NJ; ++j) w_off[j] = n0 + 32 * j + col < sN ? (n0 + 32 * j + col) * g.row_bytes : BUF_INVALID;
 
   // raw data of two k-steps in flight: A planes [set][i], weights [set][w][j][ks]
   uint4 pah[2][AI], pal[2][AI];  // (one set used when ASETS == 1)
@@ -587,17 +604,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const uint32_t n = n0 + 32 * j + col;
-    if (n >= g.N) continue;
-    const float bias = (MODE == GEMM_STORE && g.bias) ? g.bias[n] : 0.f;
+    if (n >= sN) continue;
+    const float bias = (MODE == GEMM_STORE && sbias) ? sbias[n] : 0.f;
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const uint32_t r = r0 + 32 * i + 8 * (v / 4) + 4 * (lane >> 5) + (v & 3);
         if (r >= g.P) continue;
-        const size_t o = (size_t)r * g.ldo + n;
-        if (MODE == GEMM_STORE) g.out[o] = g.bias ? acc[i][0][j][v] + bias : acc[i][0][j][v];  // model.rs:179-183
-        if (MODE == GEMM_RESID) g.out[o] = g.out[o] + acc[i][0][j][v];                         // tensor.rs:232
+        const size_t o = (size_t)r * sldo + n;
+        if (MODE == GEMM_STORE) sout[o] = sbias ? acc[i][0][j][v] + bias : acc[i][0][j][v];  // model.rs:179-183
+        if (MODE == GEMM_RESID) sout[o] = sout[o] + acc[i][0][j][v];                        // tensor.rs:232
         if (MODE == GEMM_SWIGLU) {                                                             // tensor.rs:224
           const float gg = acc[i][0][j][v];
           split1(gg / (1.0f + expf(-gg)) * acc[i][NW - 1][j][v], g.o_hi[o], g.o_lo[o]);
@@ -611,7 +628,9 @@ static hipError_t gemm_go_types(const GemmArgs& g, dim3 grid, uint32_t lds, hipS
 
 template <int MODE, int MT, int NJ>
 static hipError_t gemm_go_b3(const GemmArgs& g, hipStream_t s) {
-  dim3 grid((g.N + 128 * NJ - 1) / (128 * NJ), (g.P + 32 * MT - 1) / (32 * MT));
+  uint32_t tiles = (g.N + 128 * NJ - 1) / (128 * NJ);
+  for (uint32_t i = 0; MODE == GEMM_STORE && i < g.n_more; ++i) tiles += (g.more[i].N + 128 * NJ - 1) / (128 * NJ);
+  dim3 grid(tiles, (g.P + 32 * MT - 1) / (32 * MT));
   constexpr uint32_t lds = gemm_lds_bytes<MT>();
   if constexpr (MODE == GEMM_SWIGLU && MT == 4) {  // Q4_K only (gemm_go)
     if (g.type != T_Q4_K) return hipErrorInvalidValue;
@@ -653,6 +672,10 @@ hipError_t launch_gemm(const GemmArgs& g, GemmMode mode, hipStream_t s) {
   if (g.K % 32 || g.P == 0 || g.N == 0) return hipErrorInvalidValue;
   if ((uint64_t)g.N * g.row_bytes >= BUF_INVALID || (uint64_t)g.P * g.K * 2 >= BUF_INVALID) return hipErrorInvalidValue;
   if (mode == GEMM_SWIGLU ? (!g.o_hi || !g.o_lo) : !g.out) return hipErrorInvalidValue;
+  if (g.n_more > 2 || (g.n_more && mode != GEMM_STORE)) return hipErrorInvalidValue;
+  for (uint32_t i = 0; i < g.n_more; ++i)
+    if (!g.more[i].w || !g.more[i].out || g.more[i].N == 0 || (uint64_t)g.more[i].N * g.row_bytes >= BUF_INVALID)
+      return hipErrorInvalidValue;
   switch (mode) {
     case GEMM_STORE: return gemm_go<GEMM_STORE>(g, s);
     case GEMM_RESID: return gemm_go<GEMM_RESID>(g, s);
