@@ -104,6 +104,7 @@ struct frn_ctx {
   float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
   // the GEMM operands as bf16 hi + lo planes: rmsnorm'd x, attention rows, SwiGLU activation
   uint16_t *pf_xs = nullptr, *pf_att = nullptr, *pf_act = nullptr;
+  uint16_t* pf_kvs = nullptr;  // a layer's K and V as the prefill attention's bf16 planes (max_ctx keys)
   uint32_t* pf_ids = nullptr;
   uint32_t len = 0;           // host view of KvCache::len
   uint32_t last_next = 0xFFFFFFFFu;
@@ -153,7 +154,7 @@ static void free_ctx(frn_ctx* c) {
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->st_ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.keys_sorted, c->full.ids, c->full.ids_sorted, c->full.tmp, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_ids};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.keys_sorted, c->full.ids, c->full.ids_sorted, c->full.tmp, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_kvs, c->pf_ids};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -203,7 +204,8 @@ static hipError_t alloc_prefill(frn_ctx* x) {
   if ((e = dmalloc(&x->pf_x, P * c.hidden * 4)) || (e = dmalloc(&x->pf_q, P * qd * 4)) ||
       (e = dmalloc(&x->pf_k, P * kvd * 4)) || (e = dmalloc(&x->pf_v, P * kvd * 4)) ||
       (e = dmalloc(&x->pf_xs, P * c.hidden * 4)) || (e = dmalloc(&x->pf_att, P * qd * 4)) ||
-      (e = dmalloc(&x->pf_act, P * c.ffn * 4)) || (e = dmalloc(&x->pf_ids, P * 4)))
+      (e = dmalloc(&x->pf_act, P * c.ffn * 4)) || (e = dmalloc(&x->pf_ids, P * 4)) ||
+      (e = dmalloc(&x->pf_kvs, kv_split_elems(c.max_ctx, (uint32_t)kvd) * 2)))
     return e;
   return hipSuccess;
 }
@@ -868,8 +870,9 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
           (e = qkv(L)) ||
           (e = launch_rope_kv_rows(c->pf_q, c->pf_k, c->pf_v, c->rope, c->kcache + lo, c->vcache + lo, g.n_heads,
                                    g.n_kv_heads, g.head_dim, pos0, m, s)) ||
-          (e = launch_attn_rows(c->pf_q, c->kcache + lo, c->vcache + lo, c->pf_att, lo_of(c->pf_att, QD), g.n_heads,
-                                g.n_kv_heads, g.head_dim, pos0, m, scale, s)) ||
+          (e = launch_kv_split(c->kcache + lo, c->vcache + lo, pos0 + m, KVD, c->pf_kvs, s)) ||
+          (e = launch_attn_rows(c->pf_q, c->pf_kvs, c->pf_att, lo_of(c->pf_att, QD), g.n_heads, g.n_kv_heads,
+                                g.head_dim, pos0, m, scale, s)) ||
           (e = gemm(L.wo, nullptr, c->pf_att, QD, nullptr, c->pf_x, nullptr, H, GEMM_RESID)) ||
           (e = launch_rows_split(c->pf_x, m, H, L.ffn_norm, g.rms_eps, c->pf_xs, lo_of(c->pf_xs, H), s)) ||
           (e = gemm(L.gate, L.up, c->pf_xs, H, nullptr, nullptr, c->pf_act, g.ffn, GEMM_SWIGLU)) ||

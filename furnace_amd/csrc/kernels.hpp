@@ -150,11 +150,17 @@ hipError_t launch_embed_rows(const uint8_t* table, uint32_t type, uint32_t hidde
 hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const float* rope_cs, float* k_cache,
                                float* v_cache, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                                uint32_t pos0, uint32_t n, hipStream_t s);
-// Causal attention of n query rows at positions pos0.. over the cache; the
-// output rows [n][n_heads * head_dim] as the GEMM's bf16 planes.
-hipError_t launch_attn_rows(const float* q, const float* k_cache, const float* v_cache, uint16_t* out_hi,
-                            uint16_t* out_lo, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t pos0,
-                            uint32_t n, float scale, hipStream_t s);
+// A layer's keys 0 .. T of the cache as the attention's bf16 planes
+// (kv_split_elems(T, kvd) 16-bit values at `planes`).
+inline size_t kv_split_elems(uint32_t T, uint32_t kvd) { return 4ull * ((T + 31) / 32 * 32) * kvd; }
+hipError_t launch_kv_split(const float* k_cache, const float* v_cache, uint32_t T, uint32_t kvd, uint16_t* planes,
+                           hipStream_t s);
+// Causal attention of n query rows at positions pos0.. over keys 0 ..
+// pos0 + n (launch_kv_split's planes); the output rows [n][n_heads *
+// head_dim] as the GEMM's bf16 planes.
+hipError_t launch_attn_rows(const float* q, const uint16_t* kv_planes, uint16_t* out_hi, uint16_t* out_lo,
+                            uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t pos0, uint32_t n,
+                            float scale, hipStream_t s);
 // Argmax of the lm_head candidates into next_tok/tok, position += n.
 hipError_t launch_prefill_end(StepState* st, const uint64_t* best, uint32_t n_best, uint32_t n, hipStream_t s);
 

@@ -712,32 +712,80 @@ hipError_t launch_rope_kv_rows(float* q, const float* k, const float* v, const f
   return hipGetLastError();
 }
 
+// ---- K/V of a layer as bf16 planes for the prefill attention -------------------------
+// Keys 0 .. T: K as hi / lo planes [T][kvd] (the cache's row layout) and V
+// transposed, Vt [kvd][Tp] (Tp = T rounded up to 32, zeros past T), with
+// the keys of every 16-key group stored in the order the P.V MFMA reads
+// them: position 8h + i of a group holds key 8(i/4) + 4h + i%4.
+__host__ __device__ constexpr uint32_t kv_pos16(uint32_t j) { return 8u * ((j / 4) % 2) + 4u * (j / 8) + j % 4; }
+
+__global__ __launch_bounds__(256) void k_kv_split(const float* __restrict__ kc, const float* __restrict__ vc,
+                                                  uint32_t T, uint32_t Tp, uint32_t kvd, uint16_t* __restrict__ kh,
+                                                  uint16_t* __restrict__ kl, uint16_t* __restrict__ vth,
+                                                  uint16_t* __restrict__ vtl) {
+  const uint32_t k0 = 16 * blockIdx.x;
+  for (uint32_t d = threadIdx.x; d < kvd; d += 256) {
+    float vv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t key = k0 + j;
+      if (key < T) {
+        const float kx = kc[(size_t)key * kvd + d];
+        split1(kx, kh[(size_t)key * kvd + d], kl[(size_t)key * kvd + d]);
+        vv[kv_pos16(j)] = vc[(size_t)key * kvd + d];
+      } else {
+        vv[kv_pos16(j)] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < 16; p += 8) {
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = vv[p + i];
+      uint4 hi, lo;
+      split8(y, hi, lo);
+      *(uint4*)(vth + (size_t)d * Tp + k0 + p) = hi;
+      *(uint4*)(vtl + (size_t)d * Tp + k0 + p) = lo;
+    }
+  }
+}
+
+hipError_t launch_kv_split(const float* kc, const float* vc, uint32_t T, uint32_t kvd, uint16_t* planes,
+                           hipStream_t s) {
+  const uint32_t Tp = (T + 31) / 32 * 32;
+  uint16_t* kh = planes;
+  uint16_t* kl = kh + (size_t)Tp * kvd;
+  uint16_t* vth = kl + (size_t)Tp * kvd;
+  uint16_t* vtl = vth + (size_t)Tp * kvd;
+  hipLaunchKernelGGL(k_kv_split, dim3(Tp / 16), dim3(256), 0, s, kc, vc, T, Tp, kvd, kh, kl, vth, vtl);
+  return hipGetLastError();
+}
+
 // ---- causal attention of a block of query rows on MFMA (model.rs:371-438) ------------
 // Block (32 query rows from q0, query head h), 4 waves; wave w takes the
-// 32-key tiles w, w + 4, ... up to the block's last query position.  With
-// v_mfma_f32_32x32x2f32 (lane l supplies A[l%32][l/32] and B[l/32][l%32];
-// accumulator register v of lane l is C[8(v/4) + 4(l/32) + v%4][l%32]):
-//  - S^T (keys x queries) = K Q^T over the head dims.  Both operands take
-//    the dims in the same permuted order (half l/32 of k-step 4j + c reads
-//    dim 8j + 4(l/32) + c), so each lane loads float4s of its key row and
-//    of its query row.  Lane l then holds the scores of query l%32 for 16
-//    keys; the softmax's running max and sum are 16 in-lane values and one
-//    exchange with lane l^32.
-//  - O^T (dims x queries) += V^T P^T.  The B operand P^T is the S^T
-//    accumulator itself: k-step i takes keys 8(i/4) + 4(l/32) + i%4, the
-//    keys whose scores lane l holds in register i.  A = V^T comes from one
-//    load per lane and k-step, dims DPL*(l%32) .. +DPL of the key's row
-//    (DPL = HD/32); component t feeds M-tile t, whose row m is dim DPL*m + t.
-// The waves' partials (O, m, l) are merged in wave order through LDS.  All
-// products and sums are f32, so only the order of the sums differs from the
-// CPU path (model.rs:371-438).
+// 32-key tiles w, w + 4, ... up to the block's last query position, on
+// v_mfma_f32_32x32x16_bf16 with every operand split hi + lo (three
+// products: hi.hi, hi.lo, lo.hi).  Lane l supplies A[l%32][8(l/32) .. +8]
+// and B[8(l/32) .. +8][l%32]; register v of lane l is
+// C[8(v/4) + 4(l/32) + v%4][l%32]:
+//  - S^T (keys x queries) = K Q^T over the head dims, 16 dims per MFMA:
+//    lane l reads dims 16c + 8(l/32) .. +8 of key row l%32 (the K planes)
+//    and of query row l%32 (split once).  Lane l then holds the scores of
+//    query l%32 for 16 keys; the softmax's running max and sum are 16
+//    in-lane values and one exchange with lane l^32.
+//  - O^T (dims x queries) += V^T P^T, 16 keys per MFMA: B = P^T is lane l's
+//    own 8 scores of the half (split), k-index 8(l/32) + i standing for key
+//    8(i/4) + 4(l/32) + i%4 of the 16; A = V^T comes as 16 bytes per plane
+//    from Vt, whose keys are stored in that order.
+// The waves' partials (O, m, l) are merged in wave order through LDS.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_rows_mfma(const float* __restrict__ q, const float* __restrict__ kc,
-                                                        const float* __restrict__ vc, uint16_t* __restrict__ out_hi,
-                                                        uint16_t* __restrict__ out_lo,
+__global__ __launch_bounds__(256, 2) void k_attn_rows_mfma(const float* __restrict__ q, const uint16_t* __restrict__ kh,
+                                                        const uint16_t* __restrict__ kl, const uint16_t* __restrict__ vth,
+                                                        const uint16_t* __restrict__ vtl, uint32_t Tp,
+                                                        uint16_t* __restrict__ out_hi, uint16_t* __restrict__ out_lo,
                                                         uint32_t nh, uint32_t nkv, uint32_t pos0, uint32_t n,
                                                         float scale) {
-  constexpr int NW = 4, DPL = HD / 32, NQ = HD / 8, OLD = HD + 1;  // O rows padded against bank conflicts
+  constexpr int NW = 4, DT = HD / 32, NC = HD / 16, OLD = HD + 1;  // O rows padded against bank conflicts
   __shared__ float mls[NW][2][32];
   __shared__ float os[32 * OLD];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hh = lane >> 5, col = lane & 31;
@@ -745,32 +793,39 @@ __global__ __launch_bounds__(256) void k_attn_rows_mfma(const float* __restrict_
   const uint32_t q0 = blockIdx.x * 32, qi = q0 + col;
   const uint32_t qr = qi < n ? qi : n - 1;  // lanes past the block's rows redo row n - 1, not stored
   const uint32_t qpos = pos0 + qr, last = pos0 + min(n, q0 + 32) - 1;
-  float4 qv[NQ];
-  const float* qrow = q + (size_t)qr * qd + h * HD + 4 * hh;
+  // the lane's query dims 16c + 8 hh .. +8, split
+  bf16x8 qh_[NC], ql_[NC];
+  {
+    const float* qrow = q + (size_t)qr * qd + h * HD + 8 * hh;
 #pragma unroll
-  for (int j = 0; j < NQ; ++j) qv[j] = *(const float4*)(qrow + 8 * j);
-  f32x16 o[DPL];
+    for (int c = 0; c < NC; ++c) {
+      const float4 a = *(const float4*)(qrow + 16 * c), b = *(const float4*)(qrow + 16 * c + 4);
+      const float y[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      uint4 hi, lo;
+      split8(y, hi, lo);
+      qh_[c] = __builtin_bit_cast(bf16x8, hi);
+      ql_[c] = __builtin_bit_cast(bf16x8, lo);
+    }
+  }
+  f32x16 o[DT];
 #pragma unroll
-  for (int t = 0; t < DPL; ++t)
+  for (int t = 0; t < DT; ++t)
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
   float m = -INFINITY, lsum = 0.f;
-  const float* kbase = kc + (size_t)g * HD + 4 * hh;
-  const float* vbase = vc + (size_t)g * HD + DPL * col;
   const uint32_t ntiles = last / 32 + 1;
   for (uint32_t kt = w; kt < ntiles; kt += NW) {
     // key rows past the last query position are clamped to it (their scores are masked)
-    const float* krow = kbase + (size_t)min(kt * 32 + col, last) * kvd;
+    const size_t krow = (size_t)min(kt * 32 + col, last) * kvd + g * HD + 8 * hh;
     f32x16 sc;
 #pragma unroll
     for (int v = 0; v < 16; ++v) sc[v] = 0.f;
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      const float4 kv = *(const float4*)(krow + 8 * j);
-      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qv[j].x, sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qv[j].y, sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qv[j].z, sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qv[j].w, sc, 0, 0, 0);
+    for (int c = 0; c < NC; ++c) {
+      const bf16x8 a_h = *(const bf16x8*)(kh + krow + 16 * c), a_l = *(const bf16x8*)(kl + krow + 16 * c);
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, qh_[c], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, ql_[c], sc, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, qh_[c], sc, 0, 0, 0);
     }
     // scale and causal mask (model.rs:384-397), then the online softmax
     float mx = m;
@@ -782,7 +837,7 @@ __global__ __launch_bounds__(256) void k_attn_rows_mfma(const float* __restrict_
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float ms = mx == -INFINITY ? 0.f : mx;  // no unmasked key yet: keep the exponents finite
-    const float c = expf(m - ms);
+    const float cf = expf(m - ms);
     float ps = 0.f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -790,26 +845,27 @@ __global__ __launch_bounds__(256) void k_attn_rows_mfma(const float* __restrict_
       ps += sc[v];
     }
     ps += __shfl_xor(ps, 32, 64);
-    lsum = lsum * c + ps;
+    lsum = lsum * cf + ps;
     m = mx;
 #pragma unroll
-    for (int t = 0; t < DPL; ++t)
+    for (int t = 0; t < DT; ++t)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) o[t][v] *= c;
+      for (int v = 0; v < 16; ++v) o[t][v] *= cf;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const uint32_t key = min(kt * 32 + 8 * (i / 4) + 4 * hh + (i & 3), last);
-      const float* vrow = vbase + (size_t)key * kvd;
-      if constexpr (DPL == 4) {
-        const float4 vv = *(const float4*)vrow;
-        o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, sc[i], o[0], 0, 0, 0);
-        o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, sc[i], o[1], 0, 0, 0);
-        o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, sc[i], o[2], 0, 0, 0);
-        o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, sc[i], o[3], 0, 0, 0);
-      } else {
-        const float2 vv = *(const float2*)vrow;
-        o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, sc[i], o[0], 0, 0, 0);
-        o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, sc[i], o[1], 0, 0, 0);
+    for (int s = 0; s < 2; ++s) {
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = sc[8 * s + i];
+      uint4 phi, plo;
+      split8(y, phi, plo);
+      const bf16x8 b_h = __builtin_bit_cast(bf16x8, phi), b_l = __builtin_bit_cast(bf16x8, plo);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const size_t vo = (size_t)(g * HD + 32 * t + col) * Tp + kt * 32 + 16 * s + 8 * hh;
+        const bf16x8 a_h = *(const bf16x8*)(vth + vo), a_l = *(const bf16x8*)(vtl + vo);
+        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, b_h, o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, b_l, o[t], 0, 0, 0);
+        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, b_h, o[t], 0, 0, 0);
       }
     }
   }
@@ -830,10 +886,10 @@ __global__ __launch_bounds__(256) void k_attn_rows_mfma(const float* __restrict_
   for (int ww = 0; ww < NW; ++ww) {
     if (w == ww) {
 #pragma unroll
-      for (int t = 0; t < DPL; ++t)
+      for (int t = 0; t < DT; ++t)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          float* p = os + col * OLD + DPL * (8 * (v / 4) + 4 * hh + (v & 3)) + t;
+          float* p = os + col * OLD + 32 * t + 8 * (v / 4) + 4 * hh + (v & 3);
           *p = ww == 0 ? e * o[t][v] : *p + e * o[t][v];
         }
     }
@@ -861,17 +917,21 @@ __global__ __launch_bounds__(256) void k_attn_rows_mfma(const float* __restrict_
   }
 }
 
-hipError_t launch_attn_rows(const float* q, const float* kc, const float* vc, uint16_t* out_hi, uint16_t* out_lo,
-                            uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t pos0, uint32_t n, float scale,
-                            hipStream_t s) {
+hipError_t launch_attn_rows(const float* q, const uint16_t* kv_planes, uint16_t* out_hi, uint16_t* out_lo, uint32_t nh,
+                            uint32_t nkv, uint32_t hd, uint32_t pos0, uint32_t n, float scale, hipStream_t s) {
   if (n == 0 || nkv == 0 || nh % nkv) return hipErrorInvalidValue;
+  const uint32_t T = pos0 + n, Tp = (T + 31) / 32 * 32, kvd = nkv * hd;
+  const uint16_t* kh = kv_planes;
+  const uint16_t* kl = kh + (size_t)Tp * kvd;
+  const uint16_t* vth = kl + (size_t)Tp * kvd;
+  const uint16_t* vtl = vth + (size_t)Tp * kvd;
   dim3 grid((n + 31) / 32, nh);
   if (hd == 128)
-    hipLaunchKernelGGL((k_attn_rows_mfma<128>), grid, dim3(256), 0, s, q, kc, vc, out_hi, out_lo, nh, nkv, pos0, n,
-                       scale);
+    hipLaunchKernelGGL((k_attn_rows_mfma<128>), grid, dim3(256), 0, s, q, kh, kl, vth, vtl, Tp, out_hi, out_lo, nh, nkv,
+                       pos0, n, scale);
   else if (hd == 64)
-    hipLaunchKernelGGL((k_attn_rows_mfma<64>), grid, dim3(256), 0, s, q, kc, vc, out_hi, out_lo, nh, nkv, pos0, n,
-                       scale);
+    hipLaunchKernelGGL((k_attn_rows_mfma<64>), grid, dim3(256), 0, s, q, kh, kl, vth, vtl, Tp, out_hi, out_lo, nh, nkv,
+                       pos0, n, scale);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
