@@ -762,37 +762,80 @@ hipError_t launch_kv_split(const float* kc, const float* vc, uint32_t T, uint32_
 }
 
 // ---- causal attention of a block of query rows on MFMA (model.rs:371-438) ------------
-// Block (32 query rows from q0, query head h), 4 waves; wave w takes the
-// 32-key tiles w, w + 4, ... up to the block's last query position, on
-// v_mfma_f32_32x32x16_bf16 with every operand split hi + lo (three
-// products: hi.hi, hi.lo, lo.hi).  Lane l supplies A[l%32][8(l/32) .. +8]
-// and B[8(l/32) .. +8][l%32]; register v of lane l is
-// C[8(v/4) + 4(l/32) + v%4][l%32]:
+// Block: 128 query rows from q0 of query head h; wave w owns rows
+// q0 + 32w .. +32 and runs every 32-key tile up to its last row.  The
+// block stages each key tile once in LDS for its four waves (K rows and V^T
+// rows, both planes; the next tile's bytes load into registers while the
+// current one computes).  On v_mfma_f32_32x32x16_bf16 with every operand
+// split hi + lo (three products: hi.hi, hi.lo, lo.hi).  Lane l supplies
+// A[l%32][8(l/32) .. +8] and B[8(l/32) .. +8][l%32]; register v of lane l
+// is C[8(v/4) + 4(l/32) + v%4][l%32]:
 //  - S^T (keys x queries) = K Q^T over the head dims, 16 dims per MFMA:
-//    lane l reads dims 16c + 8(l/32) .. +8 of key row l%32 (the K planes)
-//    and of query row l%32 (split once).  Lane l then holds the scores of
-//    query l%32 for 16 keys; the softmax's running max and sum are 16
-//    in-lane values and one exchange with lane l^32.
+//    lane l takes dims 16c + 8(l/32) .. +8 of key row l%32 and of query
+//    row l%32 (split once).  Lane l then holds the scores of query l%32 for
+//    16 keys; the softmax's running max and sum are 16 in-lane values and
+//    one exchange with lane l^32.
 //  - O^T (dims x queries) += V^T P^T, 16 keys per MFMA: B = P^T is lane l's
 //    own 8 scores of the half (split), k-index 8(l/32) + i standing for key
-//    8(i/4) + 4(l/32) + i%4 of the 16; A = V^T comes as 16 bytes per plane
-//    from Vt, whose keys are stored in that order.
-// The waves' partials (O, m, l) are merged in wave order through LDS.
+//    8(i/4) + 4(l/32) + i%4 of the 16; A = V^T comes from Vt, whose keys
+//    are stored in that order.
 template <int HD>
 __global__ __launch_bounds__(256, 2) void k_attn_rows_mfma(const float* __restrict__ q, const uint16_t* __restrict__ kh,
-                                                        const uint16_t* __restrict__ kl, const uint16_t* __restrict__ vth,
-                                                        const uint16_t* __restrict__ vtl, uint32_t Tp,
-                                                        uint16_t* __restrict__ out_hi, uint16_t* __restrict__ out_lo,
-                                                        uint32_t nh, uint32_t nkv, uint32_t pos0, uint32_t n,
-                                                        float scale) {
-  constexpr int NW = 4, DT = HD / 32, NC = HD / 16, OLD = HD + 1;  // O rows padded against bank conflicts
-  __shared__ float mls[NW][2][32];
-  __shared__ float os[32 * OLD];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hh = lane >> 5, col = lane & 31;
+                                                           const uint16_t* __restrict__ kl,
+                                                           const uint16_t* __restrict__ vth,
+                                                           const uint16_t* __restrict__ vtl, uint32_t Tp,
+                                                           uint16_t* __restrict__ out_hi,
+                                                           uint16_t* __restrict__ out_lo, uint32_t nh, uint32_t nkv,
+                                                           uint32_t pos0, uint32_t n, float scale) {
+  constexpr int DT = HD / 32, NC = HD / 16;
+  constexpr int KP = HD + 8, VP = 40;  // LDS row pitches (bf16): 16-byte reads of 16 rows hit distinct banks
+  constexpr int KE = 32 * KP, VE = HD * VP;
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][2][KE];  // [buffer][plane]
+  __shared__ __attribute__((aligned(16))) uint16_t vs[2][2][VE];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, hh = lane >> 5, col = lane & 31;
   const uint32_t h = blockIdx.y, g = h / (nh / nkv), qd = nh * HD, kvd = nkv * HD;
-  const uint32_t q0 = blockIdx.x * 32, qi = q0 + col;
-  const uint32_t qr = qi < n ? qi : n - 1;  // lanes past the block's rows redo row n - 1, not stored
-  const uint32_t qpos = pos0 + qr, last = pos0 + min(n, q0 + 32) - 1;
+  const uint32_t q0 = blockIdx.x * 128, qw = q0 + 32 * w, qi = qw + col;
+  const bool wave_on = qw < n;
+  const uint32_t qr = qi < n ? qi : n - 1;  // lanes past the rows redo row n - 1, not stored
+  const uint32_t qpos = pos0 + qr;
+  const uint32_t last_w = pos0 + min(n, qw + 32) - 1, last_b = pos0 + min(n, q0 + 128) - 1;
+  // tile loaders: K row t / 8 (HD / 8 values from 16 * (t % 8) * HD / 128), V^T row
+  // t * HD / 256 (32 * HD / 256 keys)
+  constexpr int KV = HD / 8, VV = HD / 8;  // bf16 per thread per plane
+  constexpr int KL = KV / 8, VL = VV / 8;  // 16-byte loads per plane
+  const uint32_t kr = t / 8, kc0 = (t % 8) * KV;
+  const uint32_t vr = t / (256 / HD), vk0 = (t % (256 / HD)) * VV;
+  // the next tile's bytes, through buffer loads (plain loads of these
+  // arrays were kept in scratch memory by the compiler)
+  const rsrc_t rkh = make_rsrc(kh, Tp * kvd * 2), rkl = make_rsrc(kl, Tp * kvd * 2);
+  const rsrc_t rvh = make_rsrc(vth, Tp * kvd * 2), rvl = make_rsrc(vtl, Tp * kvd * 2);
+  uint4 pkh[KL], pkl[KL], pvh[VL], pvl[VL];
+  auto fetch = [&](uint32_t kt) {
+    const uint32_t ko = 2 * (min(kt * 32 + kr, last_b) * kvd + g * HD + kc0);
+    const uint32_t vo = 2 * ((g * HD + vr) * Tp + kt * 32 + vk0);
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      pkh[i] = bl128(rkh, ko + 16 * i);
+      pkl[i] = bl128(rkl, ko + 16 * i);
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      pvh[i] = bl128(rvh, vo + 16 * i);
+      pvl[i] = bl128(rvl, vo + 16 * i);
+    }
+  };
+  auto put = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < KL; ++i) {
+      *(uint4*)&ks[b][0][kr * KP + kc0 + 8 * i] = pkh[i];
+      *(uint4*)&ks[b][1][kr * KP + kc0 + 8 * i] = pkl[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      *(uint4*)&vs[b][0][vr * VP + vk0 + 8 * i] = pvh[i];
+      *(uint4*)&vs[b][1][vr * VP + vk0 + 8 * i] = pvl[i];
+    }
+  };
   // the lane's query dims 16c + 8 hh .. +8, split
   bf16x8 qh_[NC], ql_[NC];
   {
@@ -809,112 +852,89 @@ __global__ __launch_bounds__(256, 2) void k_attn_rows_mfma(const float* __restri
   }
   f32x16 o[DT];
 #pragma unroll
-  for (int t = 0; t < DT; ++t)
+  for (int tt = 0; tt < DT; ++tt)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
+    for (int v = 0; v < 16; ++v) o[tt][v] = 0.f;
   float m = -INFINITY, lsum = 0.f;
-  const uint32_t ntiles = last / 32 + 1;
-  for (uint32_t kt = w; kt < ntiles; kt += NW) {
-    // key rows past the last query position are clamped to it (their scores are masked)
-    const size_t krow = (size_t)min(kt * 32 + col, last) * kvd + g * HD + 8 * hh;
-    f32x16 sc;
+  const uint32_t ntiles = last_b / 32 + 1;
+  fetch(0);
+  put(0);
+  __syncthreads();
+  for (uint32_t kt = 0; kt < ntiles; ++kt) {
+    const int b = kt & 1;
+    if (kt + 1 < ntiles) fetch(kt + 1);
+    if (wave_on && kt * 32 <= last_w) {
+      f32x16 sc;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) sc[v] = 0.f;
+      for (int v = 0; v < 16; ++v) sc[v] = 0.f;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const bf16x8 a_h = *(const bf16x8*)(kh + krow + 16 * c), a_l = *(const bf16x8*)(kl + krow + 16 * c);
-      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, qh_[c], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, ql_[c], sc, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, qh_[c], sc, 0, 0, 0);
-    }
-    // scale and causal mask (model.rs:384-397), then the online softmax
-    float mx = m;
+      for (int c = 0; c < NC; ++c) {
+        const bf16x8 a_h = *(const bf16x8*)&ks[b][0][col * KP + 16 * c + 8 * hh];
+        const bf16x8 a_l = *(const bf16x8*)&ks[b][1][col * KP + 16 * c + 8 * hh];
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, qh_[c], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, ql_[c], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, qh_[c], sc, 0, 0, 0);
+      }
+      // scale and causal mask (model.rs:384-397), then the online softmax
+      float mx = m;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const uint32_t key = kt * 32 + 8 * (v / 4) + 4 * hh + (v & 3);
-      sc[v] = key <= qpos ? sc[v] * scale : -INFINITY;
-      mx = fmaxf(mx, sc[v]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float ms = mx == -INFINITY ? 0.f : mx;  // no unmasked key yet: keep the exponents finite
-    const float cf = expf(m - ms);
-    float ps = 0.f;
+      for (int v = 0; v < 16; ++v) {
+        const uint32_t key = kt * 32 + 8 * (v / 4) + 4 * hh + (v & 3);
+        sc[v] = key <= qpos ? sc[v] * scale : -INFINITY;
+        mx = fmaxf(mx, sc[v]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float ms = mx == -INFINITY ? 0.f : mx;  // no unmasked key yet: keep the exponents finite
+      const float cf = expf(m - ms);
+      float ps = 0.f;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      sc[v] = expf(sc[v] - ms);
-      ps += sc[v];
-    }
-    ps += __shfl_xor(ps, 32, 64);
-    lsum = lsum * cf + ps;
-    m = mx;
+      for (int v = 0; v < 16; ++v) {
+        sc[v] = expf(sc[v] - ms);
+        ps += sc[v];
+      }
+      ps += __shfl_xor(ps, 32, 64);
+      lsum = lsum * cf + ps;
+      m = mx;
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
+      for (int tt = 0; tt < DT; ++tt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) o[t][v] *= cf;
+        for (int v = 0; v < 16; ++v) o[tt][v] *= cf;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      float y[8];
+      for (int s = 0; s < 2; ++s) {
+        float y[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = sc[8 * s + i];
-      uint4 phi, plo;
-      split8(y, phi, plo);
-      const bf16x8 b_h = __builtin_bit_cast(bf16x8, phi), b_l = __builtin_bit_cast(bf16x8, plo);
+        for (int i = 0; i < 8; ++i) y[i] = sc[8 * s + i];
+        uint4 phi, plo;
+        split8(y, phi, plo);
+        const bf16x8 b_h = __builtin_bit_cast(bf16x8, phi), b_l = __builtin_bit_cast(bf16x8, plo);
 #pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const size_t vo = (size_t)(g * HD + 32 * t + col) * Tp + kt * 32 + 16 * s + 8 * hh;
-        const bf16x8 a_h = *(const bf16x8*)(vth + vo), a_l = *(const bf16x8*)(vtl + vo);
-        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, b_h, o[t], 0, 0, 0);
-        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, b_l, o[t], 0, 0, 0);
-        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, b_h, o[t], 0, 0, 0);
+        for (int tt = 0; tt < DT; ++tt) {
+          const uint32_t vo = (32 * tt + col) * VP + 16 * s + 8 * hh;
+          const bf16x8 a_h = *(const bf16x8*)&vs[b][0][vo], a_l = *(const bf16x8*)&vs[b][1][vo];
+          o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, b_h, o[tt], 0, 0, 0);
+          o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, b_l, o[tt], 0, 0, 0);
+          o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, b_h, o[tt], 0, 0, 0);
+        }
       }
     }
-  }
-  // merge: M = max over the waves, partial w weighted by e^(m_w - M)
-  if (hh == 0) {
-    mls[w][0][col] = m;
-    mls[w][1][col] = lsum;
-  }
-  __syncthreads();
-  auto weight = [&](int ww, uint32_t qq, float M) {
-    const float mw = mls[ww][0][qq];
-    return mw == -INFINITY ? 0.f : expf(mw - M);
-  };
-  float M = -INFINITY;
-#pragma unroll
-  for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mls[ww][0][col]);
-  const float e = weight(w, col, M);
-  for (int ww = 0; ww < NW; ++ww) {
-    if (w == ww) {
-#pragma unroll
-      for (int t = 0; t < DT; ++t)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          float* p = os + col * OLD + 32 * t + 8 * (v / 4) + 4 * hh + (v & 3);
-          *p = ww == 0 ? e * o[t][v] : *p + e * o[t][v];
-        }
-    }
+    if (kt + 1 < ntiles) put(b ^ 1);
     __syncthreads();
   }
-  // thread t writes query t / 8, dims [HD/8 * (t % 8), +HD/8)
-  const uint32_t qq = threadIdx.x / 8, d0 = (threadIdx.x % 8) * (HD / 8);
-  if (q0 + qq >= n) return;
-  float Mq = -INFINITY, L = 0.f;
+  // the o-proj GEMM's operand form: bf16 hi + lo planes; lane l holds dims
+  // 32t + 8(v/4) + 4(l/32) + v%4 of query l%32
+  if (!wave_on || qi >= n) return;
+  const float inv = 1.0f / lsum;
+  const size_t ob = (size_t)qi * qd + h * HD + 4 * hh;
 #pragma unroll
-  for (int ww = 0; ww < NW; ++ww) Mq = fmaxf(Mq, mls[ww][0][qq]);
+  for (int tt = 0; tt < DT; ++tt)
 #pragma unroll
-  for (int ww = 0; ww < NW; ++ww) L += weight(ww, qq, Mq) * mls[ww][1][qq];
-  // the o-proj GEMM's operand form: bf16 hi + lo planes
-  const size_t ob = (size_t)(q0 + qq) * qd + h * HD + d0;
-#pragma unroll
-  for (int d = 0; d < HD / 8; d += 8) {
-    float y[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = os[qq * OLD + d0 + d + i] / L;
-    uint4 hi, lo;
-    split8(y, hi, lo);
-    *(uint4*)(out_hi + ob + d) = hi;
-    *(uint4*)(out_lo + ob + d) = lo;
-  }
+    for (int r = 0; r < 4; ++r) {
+      uint32_t hi[2], lo[2];
+      split2(o[tt][4 * r] * inv, o[tt][4 * r + 1] * inv, hi[0], lo[0]);
+      split2(o[tt][4 * r + 2] * inv, o[tt][4 * r + 3] * inv, hi[1], lo[1]);
+      *(uint2*)(out_hi + ob + 32 * tt + 8 * r) = make_uint2(hi[0], hi[1]);
+      *(uint2*)(out_lo + ob + 32 * tt + 8 * r) = make_uint2(lo[0], lo[1]);
+    }
 }
 
 hipError_t launch_attn_rows(const float* q, const uint16_t* kv_planes, uint16_t* out_hi, uint16_t* out_lo, uint32_t nh,
@@ -925,7 +945,7 @@ hipError_t launch_attn_rows(const float* q, const uint16_t* kv_planes, uint16_t*
   const uint16_t* kl = kh + (size_t)Tp * kvd;
   const uint16_t* vth = kl + (size_t)Tp * kvd;
   const uint16_t* vtl = vth + (size_t)Tp * kvd;
-  dim3 grid((n + 31) / 32, nh);
+  dim3 grid((n + 127) / 128, nh);
   if (hd == 128)
     hipLaunchKernelGGL((k_attn_rows_mfma<128>), grid, dim3(256), 0, s, q, kh, kl, vth, vtl, Tp, out_hi, out_lo, nh, nkv,
                        pos0, n, scale);
