@@ -284,7 +284,7 @@ struct Deq8<T_F32> {
 // weight bytes of k-step t + 2 and the A planes of k-step t + 1 are in
 // flight while k-step t computes.  LDS rows of 32 bf16 are padded to 40
 // (80 bytes: the 16-byte reads of 16 consecutive rows hit distinct banks).
-constexpr int BKP = 40;
+constexpr int BKP = 56;
 template <int MT>
 __host__ __device__ constexpr uint32_t gemm_lds_bytes() {
   return 2u * 2u * 32u * MT * BKP * 2u;  // 2 buffers x 2 planes x rows x padded row
