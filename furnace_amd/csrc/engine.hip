@@ -154,7 +154,7 @@ static void free_ctx(frn_ctx* c) {
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->st_ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.keys_sorted, c->full.ids, c->full.ids_sorted, c->full.tmp, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_kvs, c->pf_ids};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.terms, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_kvs, c->pf_ids};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -1065,21 +1065,18 @@ extern "C" frn_status frn_sampler_init(frn_ctx* c, float temperature, uint32_t t
                 c->cfg.vocab, top_k, SAMPLER_MAX_SORT);
   HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
   if (full && !c->full.keys) {
-    const size_t V = c->cfg.vocab;
     SamplerFull f;
+    f.n2 = sampler_full_size(c->cfg.vocab);
     hipError_t e;
-    if ((e = sampler_full_tmp_bytes(c->cfg.vocab, &f.tmp_bytes)) || (e = dmalloc(&f.keys, V * 4)) ||
-        (e = dmalloc(&f.keys_sorted, V * 4)) || (e = dmalloc(&f.ids, V * 4)) || (e = dmalloc(&f.ids_sorted, V * 4)) ||
-        (e = dmalloc(&f.tmp, f.tmp_bytes ? f.tmp_bytes : 1))) {
-      void* ps[] = {f.keys, f.keys_sorted, f.ids, f.ids_sorted, f.tmp};
-      for (void* q : ps)
-        if (q) (void)hipFree(q);
+    if ((e = dmalloc(&f.keys, (size_t)f.n2 * 8)) || (e = dmalloc(&f.terms, (size_t)c->cfg.vocab * 4))) {
+      if (f.keys) (void)hipFree(f.keys);
       return fail(e == hipErrorOutOfMemory ? FRN_EOOM : FRN_EHIP, "frn_sampler_init: whole-vocabulary buffers: %s",
                   hipGetErrorString(e));
     }
     c->full = f;
   }
-  HIP_TRY(sampler_prepare(c->cfg.vocab, SAMPLER_MAX_K), "sampler LDS limit");
+  // the candidate path's sort for the k it will run (the whole-vocabulary path needs none)
+  if (!full) HIP_TRY(sampler_prepare(c->cfg.vocab, draw ? std::min(top_k, SAMPLER_MAX_K) : 1u), "sampler LDS limit");
   SamplerRng r{0, (0xda3e39cb94b95bdbull << 1) | 1u, 0};
   pcg32_step(r);
   r.state += seed;

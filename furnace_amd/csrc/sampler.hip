@@ -13,9 +13,10 @@
 //    PCG32 state in device memory.
 //
 // top_k 0 ("no cut") and top_k above 64 take the whole-vocabulary path:
-//  k_sample_full_keys: the penalty and temperature per logit;
-//  a stable radix sort of all (value, id) pairs by descending value
-//    (hipCUB), so equal values keep ascending ids as above;
+//  k_sample_full_keys: the penalty and temperature per logit, as unique
+//    sort keys (value descending, then id ascending);
+//  a bitonic sort of the keys (k_bitonic_run in LDS, k_bitonic_step over
+//    global memory);
 //  k_sample_full_pick: the softmax terms in parallel, then one thread runs
 //    the same sequential sums over the sorted vocabulary while the block
 //    stages each next stretch of terms (or probabilities) through LDS.
@@ -28,8 +29,6 @@
 #include "sampler.hpp"
 
 #include <math.h>
-
-#include <hipcub/hipcub.hpp>
 
 namespace frn {
 
@@ -166,16 +165,44 @@ __global__ __launch_bounds__(1024) void k_sample_pick(const float* __restrict__ 
   st->tok = pick;
 }
 
-// the penalty and temperature of every logit (as k_sample_cand), ids in order
+// ---- whole-vocabulary path (top_k 0 or above SAMPLER_MAX_K) -----------------------
+// Every candidate gets a unique 64-bit key, (descending value key << 32) |
+// id, so that ascending keys are the reference's sorted order (larger
+// scaled logit first; equal values by ascending id).  A bitonic sort puts
+// them in order: blocks sort runs of FULL_RUN keys in LDS, then every
+// merge step whose partner distance is at least FULL_RUN runs as a pass
+// over global memory and the shorter ones of each merge in LDS again.
+// The reference's sums are then taken in that order, one by one in f32,
+// as it takes them: they are not associative, and over ~10^5 small terms
+// their rounding moves the cumulative probabilities well beyond an ulp, so
+// any other summation order would pick other ids.
+constexpr uint32_t FULL_RUN = 4096;  // keys per block-local run (32 KB of LDS)
+
+__device__ __forceinline__ uint32_t order_key(float v) {  // larger v -> larger key
+  if (v == 0.0f) v = 0.0f;                                 // -0 sorts with +0: the reference compares them equal
+  const uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint64_t key) {  // the scaled logit of a sorted key
+  const uint32_t k = ~(uint32_t)(key >> 32);
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// the penalty and temperature of every logit (as k_sample_cand), as sort
+// keys; [vocab, n2) padded with keys that sort last
 __global__ __launch_bounds__(256) void k_sample_full_keys(const float* __restrict__ logits, uint32_t vocab,
-                                                          const uint32_t* __restrict__ recent, uint32_t n_recent,
-                                                          float penalty, float temperature, float* __restrict__ keys,
-                                                          uint32_t* __restrict__ ids) {
+                                                          uint32_t n2, const uint32_t* __restrict__ recent,
+                                                          uint32_t n_recent, float penalty, float temperature,
+                                                          uint64_t* __restrict__ keys) {
   __shared__ uint32_t rec[SAMPLER_MAX_RECENT];
   for (uint32_t i = threadIdx.x; i < n_recent; i += blockDim.x) rec[i] = recent[i];
   __syncthreads();
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= vocab) return;
+  if (t >= n2) return;
+  if (t >= vocab) {
+    keys[t] = ~0ull;
+    return;
+  }
   float x = logits[t];
   if (penalty != 1.0f) {  // apply_repeat_penalty (sampler.rs:39-55)
     bool hit = false;
@@ -183,9 +210,46 @@ __global__ __launch_bounds__(256) void k_sample_full_keys(const float* __restric
     if (hit) x = x > 0.0f ? x / penalty : x * penalty;
   }
   x = x / temperature;  // filtered(), sampler.rs:121-125
-  if (x == 0.0f) x = 0.0f;  // -0 sorts with +0: the reference compares them equal
-  keys[t] = x;
-  ids[t] = t;
+  keys[t] = ((uint64_t)~order_key(x) << 32) | t;
+}
+
+// bitonic steps on n2 keys, ascending where (index & k) == 0
+__device__ __forceinline__ void bitonic_cas(uint64_t& a, uint64_t& b, bool up) {
+  if ((a > b) == up) {
+    const uint64_t t = a;
+    a = b;
+    b = t;
+  }
+}
+// a run of FULL_RUN keys in LDS: the merges k = k0 .. k1 (powers of two), each
+// with its partner distances below min(k, FULL_RUN)
+__global__ __launch_bounds__(1024) void k_bitonic_run(uint64_t* __restrict__ keys, uint32_t k0, uint32_t k1) {
+  __shared__ uint64_t s[FULL_RUN];
+  const uint32_t base = blockIdx.x * FULL_RUN;
+  for (uint32_t i = threadIdx.x; i < FULL_RUN; i += blockDim.x) s[i] = keys[base + i];
+  __syncthreads();
+  for (uint32_t k = k0; k <= k1; k <<= 1)
+    for (uint32_t j = min(k, FULL_RUN) >> 1; j > 0; j >>= 1) {
+      for (uint32_t i = threadIdx.x; i < FULL_RUN / 2; i += blockDim.x) {
+        const uint32_t lo = 2 * i - (i & (j - 1)), hi = lo + j;  // the pair (lo, lo ^ j), lo's bit j clear
+        bitonic_cas(s[lo], s[hi], ((base + lo) & k) == 0);
+      }
+      __syncthreads();
+    }
+  for (uint32_t i = threadIdx.x; i < FULL_RUN; i += blockDim.x) keys[base + i] = s[i];
+}
+// one merge step with partner distance j >= FULL_RUN, over global memory
+__global__ __launch_bounds__(256) void k_bitonic_step(uint64_t* __restrict__ keys, uint32_t n2, uint32_t k,
+                                                      uint32_t j) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n2 / 2) return;
+  const uint32_t lo = 2 * i - (i & (j - 1)), hi = lo + j;
+  uint64_t a = keys[lo], b = keys[hi];
+  const bool up = (lo & k) == 0;
+  if ((a > b) == up) {
+    keys[lo] = b;
+    keys[hi] = a;
+  }
 }
 
 // Sequential passes over the sorted candidates (Sampler::filtered and the
@@ -193,29 +257,31 @@ __global__ __launch_bounds__(256) void k_sample_full_keys(const float* __restric
 // FULL_CHUNK values at a time through LDS, computing each pass's
 // per-element values (terms, terms / sum, their renormalization) in
 // parallel with the same single divisions; thread 0 then folds them in
-// order, 16 at a time: four float4 LDS reads (the next group's issued
-// before this group is added), 16 dependent f32 adds, and for the passes
-// that stop at a crossing one test per group on the last running sum (the
-// sums only grow, so the first crossing lies in the first group whose last
-// sum crosses).
+// order, 16 at a time (four float4 LDS reads, the next group's issued
+// before this group is added, then 16 dependent f32 adds).  The terms only
+// shrink along the order, so a pass also ends once a group's last term is
+// below half an ulp of the running sum: every later addition would leave
+// it unchanged.
 constexpr uint32_t FULL_CHUNK = 8192;
 constexpr int FOLD = 16;
-__global__ __launch_bounds__(1024) void k_sample_full_pick(const float* __restrict__ v, float* __restrict__ e,
-                                                           const uint32_t* __restrict__ id, uint32_t vocab,
-                                                           uint32_t k, float top_p, SamplerRng* rng,
-                                                           StepState* st) {
+__device__ __forceinline__ float half_ulp(float a) {  // a > 0, normal, exponent above -102
+  return __uint_as_float((__float_as_uint(a) & 0x7F800000u) - (24u << 23));
+}
+__global__ __launch_bounds__(1024) void k_sample_full_pick(const uint64_t* __restrict__ keys,
+                                                           float* __restrict__ e, uint32_t vocab, uint32_t k,
+                                                           float top_p, SamplerRng* rng, StepState* st) {
   __shared__ __align__(16) float buf[FULL_CHUNK];
   __shared__ float sh_val;
   __shared__ uint32_t sh_idx, sh_done;
   const uint32_t len0 = (k > 0 && k < vocab) ? k : vocab;  // top-k cut, else every candidate
-  // softmax terms e^(v_i - max), max = v_0 (sampler.rs:131-137); e is a
-  // buffer this kernel has not read, so its reads see these writes
-  const float mx = v[0];
-  for (uint32_t i = threadIdx.x; i < len0; i += blockDim.x) e[i] = (float)exp((double)(v[i] - mx));
+  // softmax terms e^(v_i - max), max = v_0 (sampler.rs:131-137)
+  const float mx = key_value(keys[0]);
+  for (uint32_t i = threadIdx.x; i < len0; i += blockDim.x) e[i] = (float)exp((double)(key_value(keys[i]) - mx));
   __syncthreads();
   // pass: stage f(i) for i < len in chunks; thread 0 runs acc += x over
   // them in order.  With `stop`, the pass ends at the first i where
-  // crossed(acc) holds and returns that i, else len.
+  // crossed(acc) holds and returns that i; else (or once the rest cannot
+  // change acc) it returns len.
   auto pass = [&](uint32_t len, float& acc, bool stop, auto&& f, auto&& crossed) -> uint32_t {
     if (threadIdx.x == 0) {
       sh_done = 0;
@@ -244,16 +310,22 @@ __global__ __launch_bounds__(1024) void k_sample_full_pick(const float* __restri
           if (g + 1 < ng)
 #pragma unroll
             for (int w = 0; w < FOLD / 4; ++w) q[w] = b4[(g + 1) * (FOLD / 4) + w];
-          float run[FOLD];
+          const float a0 = acc;
 #pragma unroll
-          for (int j = 0; j < FOLD; ++j) {
-            acc += x[j];
-            run[j] = acc;
-          }
-          if (stop && crossed(run[FOLD - 1])) {
+          for (int j = 0; j < FOLD; ++j) acc += x[j];
+          if (stop && crossed(acc)) {  // the sums only grow: the crossing lies in this group
+            float a = a0;
             int j = 0;
-            while (!crossed(run[j])) ++j;
+            for (; j < FOLD; ++j) {
+              a += x[j];
+              if (crossed(a)) break;
+            }
+            acc = a;
             sh_idx = c0 + g * FOLD + j;
+            sh_done = 1;
+            break;
+          }
+          if (x[FOLD - 1] < half_ulp(acc)) {  // the rest is absorbed: acc is final
             sh_done = 1;
             break;
           }
@@ -281,15 +353,15 @@ __global__ __launch_bounds__(1024) void k_sample_full_pick(const float* __restri
   sum = sh_val;
   uint32_t len = len0;
   float t = 1.0f;
-  if (top_p < 1.0f) {  // keep through the crossing token, then renormalize (sampler.rs:143-153)
+  if (top_p < 1.0f) {
+    // keep through the crossing token, then renormalize (sampler.rs:143-153);
+    // the renormalizing sum adds the same terms in the same order as the
+    // cumulative sum up to the crossing, so it is that cumulative sum
     float cum = 0.0f;
     const uint32_t at = pass(len0, cum, true, [&](uint32_t i) { return e[i] / sum; },
                              [&](float c) { return c >= top_p; });
-    __syncthreads();
     len = at < len0 ? at + 1 : len0;
-    float s2 = 0.0f;
-    pass(len, s2, false, [&](uint32_t i) { return e[i] / sum; }, never);
-    if (threadIdx.x == 0) sh_val = s2;
+    if (threadIdx.x == 0) sh_val = cum;
     __syncthreads();
     t = sh_val;
   }
@@ -306,7 +378,7 @@ __global__ __launch_bounds__(1024) void k_sample_full_pick(const float* __restri
   const uint32_t at = pass(len, cum, true, [&](uint32_t i) { const float p = e[i] / sum; return renorm ? p / t : p; },
                            [&](float c) { return u < c; });
   if (threadIdx.x == 0) {
-    const uint32_t pick = id[at < len ? at : len - 1];  // candidates.last() when the sum never passes u
+    const uint32_t pick = (uint32_t)keys[at < len ? at : len - 1];  // candidates.last() when the sum never passes u
     st->next_tok = pick;
     st->tok = pick;
   }
@@ -316,26 +388,27 @@ __global__ __launch_bounds__(1024) void k_sample_full_pick(const float* __restri
 
 uint32_t sampler_blocks(uint32_t vocab) { return (vocab + CAND_BLOCK - 1) / CAND_BLOCK; }
 
-hipError_t sampler_full_tmp_bytes(uint32_t vocab, size_t* bytes) {
-  *bytes = 0;
-  return hipcub::DeviceRadixSort::SortPairsDescending(nullptr, *bytes, (const float*)nullptr, (float*)nullptr,
-                                                      (const uint32_t*)nullptr, (uint32_t*)nullptr, (int)vocab);
+uint32_t sampler_full_size(uint32_t vocab) {
+  uint32_t n2 = FULL_RUN;
+  while (n2 < vocab) n2 <<= 1;
+  return n2;
 }
 
 hipError_t launch_sample_full(const float* logits, uint32_t vocab, const uint32_t* recent, uint32_t n_recent,
                               float penalty, float temperature, uint32_t k, float top_p, const SamplerFull& f,
                               SamplerRng* rng, StepState* st, hipStream_t s) {
-  if (n_recent > SAMPLER_MAX_RECENT || !f.keys || !f.tmp || vocab == 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_sample_full_keys, dim3((vocab + 255) / 256), dim3(256), 0, s, logits, vocab, recent, n_recent,
-                     penalty, temperature, f.keys, f.ids);
-  hipError_t e = hipGetLastError();
-  if (e) return e;
-  size_t bytes = f.tmp_bytes;
-  if ((e = hipcub::DeviceRadixSort::SortPairsDescending(f.tmp, bytes, f.keys, f.keys_sorted, f.ids, f.ids_sorted,
-                                                        (int)vocab, 0, 32, s)))
-    return e;
-  hipLaunchKernelGGL(k_sample_full_pick, dim3(1), dim3(1024), 0, s, f.keys_sorted, f.keys, f.ids_sorted, vocab, k,
-                     top_p, rng, st);
+  const uint32_t n2 = sampler_full_size(vocab);
+  if (n_recent > SAMPLER_MAX_RECENT || !f.keys || !f.terms || vocab == 0 || n2 > f.n2) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_sample_full_keys, dim3((n2 + 255) / 256), dim3(256), 0, s, logits, vocab, n2, recent, n_recent,
+                     penalty, temperature, f.keys);
+  // bitonic sort: runs of FULL_RUN in LDS, then each longer merge's global steps and its LDS tail
+  hipLaunchKernelGGL(k_bitonic_run, dim3(n2 / FULL_RUN), dim3(1024), 0, s, f.keys, 2u, FULL_RUN);
+  for (uint32_t kk = 2 * FULL_RUN; kk <= n2; kk <<= 1) {
+    for (uint32_t j = kk / 2; j >= FULL_RUN; j >>= 1)
+      hipLaunchKernelGGL(k_bitonic_step, dim3((n2 / 2 + 255) / 256), dim3(256), 0, s, f.keys, n2, kk, j);
+    hipLaunchKernelGGL(k_bitonic_run, dim3(n2 / FULL_RUN), dim3(1024), 0, s, f.keys, kk, kk);
+  }
+  hipLaunchKernelGGL(k_sample_full_pick, dim3(1), dim3(1024), 0, s, f.keys, f.terms, vocab, k, top_p, rng, st);
   return hipGetLastError();
 }
 

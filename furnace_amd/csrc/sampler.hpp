@@ -29,18 +29,16 @@ hipError_t launch_sample(const float* logits, uint32_t vocab, const uint32_t* re
                          uint32_t* cand_id, SamplerRng* rng, StepState* st, hipStream_t s);
 
 // The whole-vocabulary path, for top_k 0 ("no cut") and top_k above
-// SAMPLER_MAX_K: every candidate sorted, then the reference's sequential
-// softmax sum, top-p cumulative sum, renormalization and draw.  Buffers of
-// `vocab` entries and the radix sort's temporary storage.
+// SAMPLER_MAX_K: every candidate sorted (sort keys of sampler_full_size
+// entries), then the reference's sequential softmax sum, top-p cumulative
+// sum and draw (terms of `vocab` entries).
 struct SamplerFull {
-  float* keys = nullptr;         // scaled logits, then the softmax terms
-  float* keys_sorted = nullptr;  // scaled logits in descending order
-  uint32_t* ids = nullptr;
-  uint32_t* ids_sorted = nullptr;
-  void* tmp = nullptr;
-  size_t tmp_bytes = 0;
+  uint64_t* keys = nullptr;  // (descending value key << 32) | id
+  float* terms = nullptr;    // softmax terms in sorted order
+  uint32_t n2 = 0;           // keys' capacity
 };
-hipError_t sampler_full_tmp_bytes(uint32_t vocab, size_t* bytes);
+// the sort's size for a vocabulary: a power of two, at least one LDS run
+uint32_t sampler_full_size(uint32_t vocab);
 hipError_t launch_sample_full(const float* logits, uint32_t vocab, const uint32_t* recent, uint32_t n_recent,
                               float penalty, float temperature, uint32_t k, float top_p, const SamplerFull& f,
                               SamplerRng* rng, StepState* st, hipStream_t s);
