@@ -159,6 +159,8 @@ def main():
     ap.add_argument("--gguf", default=None, help="use this GGUF instead of writing the synthetic one")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one (for profilers) instead of "
                     "replaying the captured decode graph")
+    ap.add_argument("--engine", choices=["auto", "graphs", "resident"], default="auto",
+                    help="decode engine: the per-step graphs, the resident decode kernel, or the engine's choice")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES, 5 times (calibrates the HBM byte "
                          "counters of rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE against a known size), then exit")
@@ -196,7 +198,11 @@ def main():
     max_ctx = args.prompt + args.steps + args.timing_steps + max(args.warmup, 8) + 2
 
     t0 = time.perf_counter()
-    model = fa.Model(path, max_ctx=max_ctx, eager=args.eager)
+    model = fa.Model(path, max_ctx=max_ctx, eager=args.eager,
+                     resident={"auto": None, "graphs": False, "resident": True}[args.engine])
+    engine_on, engine_why = model.decode_engine()
+    log("decode engine: %s%s" % ("resident kernel" if engine_on else "step graphs",
+                                  "" if engine_on else " (%s)" % engine_why))
     log("weights uploaded in %.2f s" % (time.perf_counter() - t0))
     w_bytes, kv_per_pos, per, lm_bytes = algorithmic_bytes(model)
     hip = fa.Hip()
@@ -323,7 +329,8 @@ def main():
                    "decode_tokens": args.steps, "bytes_per_token": int(step_bytes),
                    "hbm_frac_per_token": round(step_gbs / HBM_PEAK_GBS, 4),
                    "prefill_tokens_per_s": round(args.prompt / prefill_s, 1),
-                   "decode_api": "frn_decode_greedy (batches of 32 steps per host sync)",
+                   "decode_api": "frn_decode_greedy (%s)" % ("resident decode kernel, 128 steps per launch"
+                                                             if engine_on else "step graphs, 32 steps per host sync"),
                    "per_call_decode_tokens_per_s": round(1000.0 / loop_ms, 1)},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": dk["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,

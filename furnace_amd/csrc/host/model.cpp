@@ -112,6 +112,10 @@ extern "C" frn_status frn_model_load(const frn_gguf* g, int device, uint32_t max
       break;
     }
     uint64_t in = t.dims.empty() ? 1 : t.dims[0];
+    if (in == 0) {  // a zero-length row would divide by zero below; Model::load errors on such shapes
+      st = frn_fail(FRN_ESHAPE, "tensor '%s': dimension 0 is zero", t.name.c_str());
+      break;
+    }
     uint64_t outd = t.dims.size() > 1 ? t.n_elements() / in : 1;
     if ((st = frn_upload(ctx, t.name.c_str(), t.type, outd, in, p, bytes))) break;
   }

@@ -2,6 +2,7 @@
 synthetic GGUF models: last-position logits within 1e-3 max-abs, KV cache
 rows, and greedy (temperature 0) ids identical for the first 32 tokens."""
 import os
+import struct
 
 import numpy as np
 import pytest
@@ -95,6 +96,23 @@ def test_errors_from_the_device_context(hip, tmpdir_models):
     assert m.cache_len() == 0
     m.prefill([1, 2])
     m.close()
+
+
+def test_load_rejects_a_zero_row_length(hip, tmpdir_models):
+    """A 2-D tensor whose first dimension is 0 is refused with FRN_ESHAPE
+    (Model::load errors on it, src/model.rs:111-123), not a division by
+    zero."""
+    path = os.path.join(tmpdir_models, "zero-dim.gguf")
+    fa.synth_write(path, seed=2, **small_models()["tiny-q4_k_m"])
+    data = bytearray(open(path, "rb").read())
+    name = b"blk.0.ffn_gate.weight"
+    at = data.index(struct.pack("<Q", len(name)) + name) + 8 + len(name)
+    assert struct.unpack_from("<I", data, at)[0] == 2  # n_dims
+    struct.pack_into("<Q", data, at + 4, 0)  # dims[0] = 0
+    open(path, "wb").write(bytes(data))
+    with pytest.raises(fa.FrnError) as e:
+        fa.Model(path, max_ctx=8)
+    assert e.value.status == 3 and "dimension 0 is zero" in str(e.value)
 
 
 def _greedy_parity(path, prompt, max_new, max_ctx):
