@@ -17,16 +17,28 @@ uint32_t attention_splits(uint32_t max_ctx, uint32_t cap) {
 // ---- reductions -----------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) { return group_reduce<64>(v); }
 __device__ __forceinline__ float wave_max(float v) { return group_reduce<64>(v, OpMax()); }
-// Sum over a 256-thread block; every thread gets the result.
-__device__ __forceinline__ float block_sum256(float v, float* red4) {
+// Sum over a block of NW waves, in wave order; every thread gets the result.
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
   v = wave_sum(v);
   int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red4[w] = v;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
   __syncthreads();
-  float r = red4[0] + red4[1] + red4[2] + red4[3];
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) r += red[i];
   __syncthreads();
   return r;
 }
+
+// GEMV blocks: NT threads (4 waves, two blocks per CU, for in <= 4096; 8
+// waves, one block per CU, for the long in of the FFN down projection, so
+// each CU stages its 35 KB of activations once and every thread converts
+// half as many values).  Whether x is staged as int8 digits (in <= 4096,
+// where the rmsnorm also occurs) and whether the f32 form is padded
+// (xf_pad4; with 4-wave blocks only while two blocks per CU still fit).
+__host__ __device__ constexpr bool gemv_dig(int nx, int nt) { return nx * 8 * nt <= 4096; }
+__host__ __device__ constexpr bool gemv_pad(int nx, int nt) { return !gemv_dig(nx, nt) && (nt >= 512 || nx <= 5); }
 
 // ---- dequant (quant.rs:261-281), bit-exact -------------------------------
 __global__ void k_dequant(uint32_t type, const uint8_t* __restrict__ raw, size_t n, float* __restrict__ out) {
@@ -52,7 +64,7 @@ hipError_t launch_dequant(uint32_t type, const uint8_t* raw, size_t n, float* ou
 
 
 // ---- activation staging ------------------------------------------------------
-// Thread t owns the 8-value groups u = t + 256 i (i < NX) of x.  Their loads
+// Thread t owns the 8-value groups u = t + NT i (i < NX) of x.  Their loads
 // (and the rmsnorm gain's) are issued first, before any weight load, so the
 // staging waits only on them while the first weight batch stays in flight.
 __device__ __forceinline__ float4 u4f(uint4 v) {
@@ -62,7 +74,7 @@ __device__ __forceinline__ float4 u4f(uint4 v) {
 // the int8 form); DSUM: they read the chunks' digit sums (Q6_K and the
 // formats not known to skip them; Q4_K and Q8_0 read only the chunk
 // scale and sum(x)).
-template <int NX, bool NORM, bool ATT, bool DIG, bool PAD = false, bool XF = true, bool DSUM = true>
+template <int NX, bool NORM, bool ATT, bool DIG, bool PAD = false, bool XF = true, bool DSUM = true, int NT = 256>
 struct XStage {
   // ATT: x is the attention output, merged here from the per-split partials
   // (o, m, l) of the attention kernel: NB splits are loaded up front with
@@ -82,7 +94,7 @@ struct XStage {
     pstride = 4u * (a.att_hd + 2);
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      const uint32_t u = threadIdx.x + 256u * i, h = 8u * u / a.att_hd, d0 = 8u * u % a.att_hd;
+      const uint32_t u = threadIdx.x + (uint32_t)NT * i, h = 8u * u / a.att_hd, d0 = 8u * u % a.att_hd;
       pbase[i] = u < a.in / 8 ? 4u * (h * a.att_ms * (a.att_hd + 2) + d0) : BUF_INVALID;
       pml[i] = 4u * (a.att_hd - d0);
     }
@@ -160,7 +172,7 @@ struct XStage {
   __device__ __forceinline__ void load(rsrc_t rx, rsrc_t rn) {
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      const uint32_t o = 32u * (threadIdx.x + 256u * i);
+      const uint32_t o = 32u * (threadIdx.x + (uint32_t)NT * i);
       x[i][0] = u4f(bl128(rx, o));
       x[i][1] = u4f(bl128(rx, o + 16u));
       if (NORM) {
@@ -184,14 +196,14 @@ struct XStage {
 #pragma unroll
         for (int h = 0; h < 2; ++h) ss += x[i][h].x * x[i][h].x + x[i][h].y * x[i][h].y + x[i][h].z * x[i][h].z +
                                           x[i][h].w * x[i][h].w;
-      ss = block_sum256(ss, red4);
+      ss = block_sum<NT / 64>(ss, red4);
       inv = 1.0f / sqrtf(ss / (float)K + eps);
     }
     const uint32_t n16 = K / 16;
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      if (256u * i >= K / 8) break;  // block-uniform: no thread has group i
-      const uint32_t u = threadIdx.x + 256u * i;
+      if ((uint32_t)NT * i >= K / 8) break;  // block-uniform: no thread has group i
+      const uint32_t u = threadIdx.x + (uint32_t)NT * i;
       const bool live = u < K / 8;
       float4 a = x[i][0], b = x[i][1];
       if (NORM && norm) {
@@ -265,14 +277,14 @@ struct XStage {
 #ifndef GEMV_MAX_GRID
 #define GEMV_MAX_GRID 512
 #endif
-// A block stages x (and applies the rmsnorm) once; then each of its 4 waves
-// works alone through "units" of G = 64 / LPR rows, one group of LPR lanes
-// per row (SWIGLU: per gate/up row pair).  Wave w of block b takes units
-// 4b + w, 4b + w + 4 * nblk, ...  A unit is S steps; in step s lane gl of a
+// A block stages x (and applies the rmsnorm) once; then each of its NW =
+// NT / 64 waves works alone through "units" of G = 64 / LPR rows, one group
+// of LPR lanes per row (SWIGLU: per gate/up row pair).  Wave w of block b
+// takes units NW b + w, NW b + w + NW nblk, ...  A unit is S steps; in step s lane gl of a
 // row loads items (s * BI + j) * LPR + gl, j < BI.  The steps of all the
 // wave's units form one flat pipeline: the loads of step f + 1 are issued
 // before step f is computed, and the first step's before the staging.
-template <uint32_t T, int LPR, int MODE, int NX, bool NORM, bool ONE>
+template <uint32_t T, int LPR, int MODE, int NX, bool NORM, bool ONE, int NT>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, uint32_t blk, uint32_t nblk,
                                           float* xf, uint8_t* pl, float* red4, uint64_t* best_s) {
   using F = Fmt<T>;
@@ -289,11 +301,11 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   // where each block would otherwise split 8960+ values into digits.
   // Measured per launch (1.5B): down 11.6 -> 9.8 us with the f32 form;
   // gate_up 9.9 vs 11.3 and o_proj 6.2 vs 6.7 us in favour of the digits.
-  constexpr bool DIG = NX <= 2;
+  constexpr bool DIG = gemv_dig(NX, NT);
+  constexpr int NW = NT / 64;
   using XT = typename std::conditional<DIG, XC, XF>::type;
-  // the f32 form stages x padded (xf_pad4) for the K-quant items while the
-  // padded x leaves room for 2 blocks per CU (in <= 10240, NX <= 5)
-  constexpr bool PAD = !DIG && NX <= 5 && (T == T_Q4_K || T == T_Q6_K);
+  // the f32 form stages x padded (xf_pad4) for the K-quant items (gemv_pad)
+  constexpr bool PAD = gemv_pad(NX, NT) && (T == T_Q4_K || T == T_Q6_K);
   // the wave index through readfirstlane: the compiler then knows every
   // per-wave quantity below is uniform (scalar loop control, no exec masks)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -301,7 +313,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   const bool pr = ((a.in / 32) % 2) == 0;
   const int n_items = items_per_row(T, a.in, pr);
   const uint32_t S = (uint32_t)(n_items + LPR * BI - 1) / (LPR * BI);
-  const uint32_t n_units = (sg.rows + G - 1) / G, stride = 4 * nblk, u0 = 4 * blk + wave;
+  const uint32_t n_units = (sg.rows + G - 1) / G, stride = NW * nblk, u0 = NW * blk + wave;
   const uint32_t n_steps = u0 < n_units ? (n_units - u0 + stride - 1) / stride * S : 0;
   const uint32_t wbytes = sg.rows * sg.row_bytes;
   const rsrc_t rw = make_rsrc(sg.w, wbytes), rw2 = make_rsrc(R == 2 ? sg.w2 : sg.w, wbytes);
@@ -309,7 +321,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
   const rsrc_t rex = make_rsrc(exp_, exp_ ? sg.rows * 4 : 0);
   const XLds X{xf, pl, a.in};
 
-  XStage<NX, NORM, ATT, DIG, PAD, !(T == T_Q4_K || T == T_Q6_K), !(T == T_Q4_K || T == T_Q8_0)> xs;
+  XStage<NX, NORM, ATT, DIG, PAD, !(T == T_Q4_K || T == T_Q6_K), !(T == T_Q4_K || T == T_Q8_0), NT> xs;
   const rsrc_t rp = make_rsrc(a.att_part, ATT ? a.att_part_bytes : 0);
   if (ATT)
     xs.load_att(a, rp);
@@ -442,7 +454,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
     __syncthreads();
     if (threadIdx.x == 0) {
       uint64_t b = best_s[0];
-      for (int i = 1; i < 4; ++i) b = best_s[i] > b ? best_s[i] : b;
+      for (int i = 1; i < NW; ++i) b = best_s[i] > b ? best_s[i] : b;
       a.best[blockIdx.x] = b;
     }
   }
@@ -453,16 +465,16 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, const GemvSeg& sg, 
 // NX: 8-value groups of x per thread (in <= 2048 * NX); NORM: rmsnorm
 // support (only the small-in kernels, where the norms occur).  MODE
 // GEMV_RESID_ATT stages x from the attention partials (in <= 4096).
-template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX, bool ONE>
-__global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
-  constexpr bool NORM = NX <= 2;
+template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX, bool ONE, int NT>
+__global__ __launch_bounds__(NT, 512 / NT) void k_gemv(GemvArgs a) {
+  constexpr bool NORM = gemv_dig(NX, NT);
   extern __shared__ float4 smem4[];
-  __shared__ float red4[4];
-  __shared__ uint64_t best_s[4];
+  __shared__ float red4[NT / 64];
+  __shared__ uint64_t best_s[NT / 64];
   // LDS: x[in] f32 | 4 byte planes of in bytes (digits, metadata); the f32
   // form: x (padded as xf_pad4 room for NX <= 5) | the in/16 chunk sums
   float* xf = (float*)smem4;
-  uint8_t* pl = (uint8_t*)(xf + (NX > 2 && NX <= 5 ? xf_padded_floats(a.in) : a.in));
+  uint8_t* pl = (uint8_t*)(xf + (gemv_pad(NX, NT) ? xf_padded_floats(a.in) : a.in));
   // Only STORE launches carry several segments (launch_gemv checks): the
   // other modes read segment 0's fields at constant offsets, in the same
   // round trip as the rest of the arguments, not after a segment search.
@@ -474,9 +486,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
   const uint32_t blk = ONESEG ? blockIdx.x : blockIdx.x - sg.block0;
   const uint32_t nblk = ONESEG ? gridDim.x : (si + 1 < a.n_seg ? a.seg[si + 1].block0 : gridDim.x) - sg.block0;
   if (T0 == T1 || sg.type == T0)
-    gemv_body<T0, LPR, MODE, NX, NORM, ONE>(a, sg, blk, nblk, xf, pl, red4, best_s);
+    gemv_body<T0, LPR, MODE, NX, NORM, ONE, NT>(a, sg, blk, nblk, xf, pl, red4, best_s);
   else
-    gemv_body<T1, LPR, MODE, NX, NORM, ONE>(a, sg, blk, nblk, xf, pl, red4, best_s);
+    gemv_body<T1, LPR, MODE, NX, NORM, ONE, NT>(a, sg, blk, nblk, xf, pl, red4, best_s);
 }
 
 // LDS of a launch: x as f32, then the int8 form's 4 planes of `in` bytes
@@ -484,8 +496,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv(GemvArgs a) {
 // in <= 10240.
 size_t gemv_lds_bytes(uint32_t in, bool) {
   if (in <= 4096) return (size_t)in * 8 + in / 4;
-  return (size_t)(in <= 10240 ? xf_padded_floats(in) : in) * 4 + in / 4;
+  return (size_t)xf_padded_floats(in) * 4 + in / 4;  // 8-wave blocks: padded f32 form
 }
+// threads per block of a launch with input length in
+static uint32_t gemv_threads(uint32_t in) { return in <= 4096 ? 256u : 512u; }
 
 
 // Lanes per row: the choice in {16, 32, 64} with the shortest critical
@@ -496,13 +510,13 @@ size_t gemv_lds_bytes(uint32_t in, bool) {
 // steps; 32 lanes -> 4480 units of 1 step, 3 steps.
 static uint32_t max_blocks(uint32_t in);
 static int lanes_per_row(uint32_t total_rows, uint32_t in, uint32_t type, int mode, int n_items) {
-  const uint32_t cap_waves = 4 * max_blocks(in);
+  const uint32_t nw = gemv_threads(in) / 64, cap_waves = nw * max_blocks(in);
   int best_l = 16;
   uint64_t best = ~0ull;
   for (int l = 16; l <= 64; l *= 2) {
     const uint32_t slots = (uint32_t)(l * gemv_bi(type, mode)), steps = ((uint32_t)n_items + slots - 1) / slots;
     const uint32_t units = (total_rows + 64 / l - 1) / (64 / l);
-    const uint32_t waves = std::min(4 * ((units + 3) / 4), cap_waves);
+    const uint32_t waves = std::min(nw * ((units + nw - 1) / nw), cap_waves);
     const uint64_t cost = (uint64_t)((units + waves - 1) / waves) * steps;
     if (cost < best) {
       best = cost;
@@ -512,10 +526,11 @@ static int lanes_per_row(uint32_t total_rows, uint32_t in, uint32_t type, int mo
   return best_l;
 }
 
-// Grid cap: 2 blocks (8 waves) per CU for in <= 10240, 1 above.  (A cap
-// of 4 per CU, which LDS would allow for small in, measured no faster: the
-// kernels are VALU-bound, not short of waves.)
+// Grid cap: 2 blocks (8 waves) per CU for in <= 4096, one 8-wave block per
+// CU above.  (A cap of 4 per CU, which LDS would allow for small in,
+// measured no faster: the kernels are VALU-bound, not short of waves.)
 static uint32_t max_blocks(uint32_t in) {
+  if (gemv_threads(in) == 512) return 256;
   const size_t lds = gemv_lds_bytes(in, false);
   return lds > 80 * 1024 ? 256 : lds > 40 * 1024 ? 512 : GEMV_MAX_GRID;
 }
@@ -523,10 +538,10 @@ static uint32_t max_blocks(uint32_t in) {
 // Blocks per segment in proportion to its units of 64 / LPR rows; each
 // block runs 4 wave workers; at most as many blocks as are resident at once.
 static uint32_t plan_blocks(GemvArgs& a, uint32_t rows_per_unit) {
-  uint32_t want[3], total = 0, cap = max_blocks(a.in);
+  uint32_t want[3], total = 0, cap = max_blocks(a.in), nw = gemv_threads(a.in) / 64;
   for (int i = 0; i < a.n_seg; ++i) {
     uint32_t units = (a.seg[i].rows + rows_per_unit - 1) / rows_per_unit;
-    want[i] = (units + 3) / 4;
+    want[i] = (units + nw - 1) / nw;
     total += want[i];
   }
   uint32_t grid = total < cap ? total : cap, used = 0;
@@ -542,23 +557,24 @@ static uint32_t plan_blocks(GemvArgs& a, uint32_t rows_per_unit) {
 
 uint32_t gemv_blocks(uint32_t type, uint32_t rows, uint32_t in) {
   int lpr = lanes_per_row(rows, in, type, GEMV_STORE, items_per_row(type, in, ((in / 32) % 2) == 0));
-  uint32_t units = (rows + 64 / lpr - 1) / (64 / lpr), want = (units + 3) / 4, cap = max_blocks(in);
+  const uint32_t nw = gemv_threads(in) / 64;
+  uint32_t units = (rows + 64 / lpr - 1) / (64 / lpr), want = (units + nw - 1) / nw, cap = max_blocks(in);
   return want < cap ? want : cap;
 }
 
-template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX, bool ONE>
+template <uint32_t T0, uint32_t T1, int LPR, int MODE, int NX, bool ONE, int NT = 256>
 static hipError_t go(GemvArgs a, hipStream_t s, uint32_t* nblocks) {
   uint32_t total = plan_blocks(a, 64 / LPR);
   if (nblocks) *nblocks = total;
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL((k_gemv<T0, T1, LPR, MODE, NX, ONE>), dim3(total), dim3(256), gemv_lds_bytes(a.in, false), s,
+  hipLaunchKernelGGL((k_gemv<T0, T1, LPR, MODE, NX, ONE, NT>), dim3(total), dim3(NT), gemv_lds_bytes(a.in, false), s,
                      a);
   return hipGetLastError();
 }
 
-// in <= 4096 (the hidden-size inputs, with or without rmsnorm) or, without
-// rmsnorm and only for STORE/RESID, in <= 20480 (the FFN down projection;
-// NX 5 up to 10240, whose padded x stays under 64 KiB of LDS, NX 10 above).
+// in <= 4096 (the hidden-size inputs, with or without rmsnorm; 4-wave
+// blocks) or, without rmsnorm and only for STORE/RESID, in <= 20480 (the
+// FFN down projection; 8-wave blocks, NX 3 up to 12288, NX 5 above).
 template <uint32_t T0, uint32_t T1, int MODE, int LPR>
 static hipError_t pick_nx(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
   const int n_items = items_per_row(T0, a.in, ((a.in / 32) % 2) == 0);
@@ -566,8 +582,8 @@ static hipError_t pick_nx(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
   if (a.in <= 2048) return one ? go<T0, T1, LPR, MODE, 1, true>(a, s, nb) : go<T0, T1, LPR, MODE, 1, false>(a, s, nb);
   if (a.in <= 4096) return one ? go<T0, T1, LPR, MODE, 2, true>(a, s, nb) : go<T0, T1, LPR, MODE, 2, false>(a, s, nb);
   if constexpr (MODE == GEMV_STORE || MODE == GEMV_RESID) {
-    if (a.norm_w == nullptr && a.in <= 10240) return go<T0, T1, LPR, MODE, 5, false>(a, s, nb);
-    if (a.norm_w == nullptr && a.in <= 20480) return go<T0, T1, LPR, MODE, 10, false>(a, s, nb);
+    if (a.norm_w == nullptr && a.in <= 12288) return go<T0, T1, LPR, MODE, 3, false, 512>(a, s, nb);
+    if (a.norm_w == nullptr && a.in <= 20480) return go<T0, T1, LPR, MODE, 5, false, 512>(a, s, nb);
   }
   return hipErrorInvalidValue;
 }
@@ -637,14 +653,16 @@ hipError_t launch_gemv(GemvArgs a, GemvMode mode, hipStream_t s, uint32_t* nb) {
   return hipErrorInvalidValue;
 }
 
-// Only the in > 4096 kernels (NX = 10) use more than the default 64 KiB of
-// dynamic LDS.
+// Only the in > 4096 kernels (8-wave blocks, NX 3 and 5) can use more than
+// the default 64 KiB of dynamic LDS.
 template <uint32_t T0, uint32_t T1, int LPR>
 static hipError_t prep_one(int bytes) {
   hipError_t e;
   const auto attr = hipFuncAttributeMaxDynamicSharedMemorySize;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 10, false>, attr, bytes))) return e;
-  return hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 10, false>, attr, bytes);
+  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 3, false, 512>, attr, bytes))) return e;
+  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 5, false, 512>, attr, bytes))) return e;
+  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 3, false, 512>, attr, bytes))) return e;
+  return hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 5, false, 512>, attr, bytes);
 }
 
 template <uint32_t T0, uint32_t T1>
