@@ -112,7 +112,12 @@ struct frn_ctx {
   // captured steps: [0] short contexts, [1] past ATTENTION_LONG_FROM positions
   hipGraphExec_t g_step[2] = {}, g_prefill[2] = {}, g_multi[2] = {};
   hipGraph_t graph_step[2] = {}, graph_prefill[2] = {}, graph_multi[2] = {};
+  // short-context steps by their exact attention split count n (T in
+  // (64 (n - 1), 64 n]): index n - 1; one step, and GREEDY_MULTI steps
+  hipGraphExec_t g_exact[ATTENTION_MAX_SPLITS] = {}, g_exact_multi[ATTENTION_MAX_SPLITS] = {};
+  hipGraph_t graph_exact[ATTENTION_MAX_SPLITS] = {}, graph_exact_multi[ATTENTION_MAX_SPLITS] = {};
   bool rec_long = false;  // the form record_step records (long-context attention)
+  uint32_t rec_splits = 0;  // > 0: record the short form with exactly this many splits
   float* att = nullptr;   // [n_heads * head_dim] merged attention output (long-context form)
   // --timings: the step runs eagerly with an event pair around each kernel
   bool timing = false;
@@ -150,6 +155,12 @@ static void free_ctx(frn_ctx* c) {
     if (c->graph_prefill[i]) (void)hipGraphDestroy(c->graph_prefill[i]);
     if (c->g_multi[i]) (void)hipGraphExecDestroy(c->g_multi[i]);
     if (c->graph_multi[i]) (void)hipGraphDestroy(c->graph_multi[i]);
+  }
+  for (uint32_t i = 0; i < ATTENTION_MAX_SPLITS; ++i) {
+    if (c->g_exact[i]) (void)hipGraphExecDestroy(c->g_exact[i]);
+    if (c->graph_exact[i]) (void)hipGraphDestroy(c->graph_exact[i]);
+    if (c->g_exact_multi[i]) (void)hipGraphExecDestroy(c->g_exact_multi[i]);
+    if (c->graph_exact_multi[i]) (void)hipGraphDestroy(c->graph_exact_multi[i]);
   }
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -447,7 +458,8 @@ static hipError_t record_step(frn_ctx* c, bool with_logits, Tick& tk) {
     size_t lo = (size_t)l * g.max_ctx * g.n_kv_heads * g.head_dim;
     const uint32_t cap = c->rec_long ? ATTENTION_MAX_SPLITS_LONG : ATTENTION_MAX_SPLITS;
     if (TIMED(CAT_ATTN, launch_attention(c->q, c->k, c->v, c->rope_cur, c->kcache + lo, c->vcache + lo, g.n_heads,
-                                         g.n_kv_heads, g.head_dim, g.max_ctx, scale, c->part, c->st, cap, s)))
+                                         g.n_kv_heads, g.head_dim, g.max_ctx, scale, c->part, c->st, cap,
+                                         c->rec_long ? 0u : c->rec_splits, s)))
       return e;
     if (c->rec_long) {
       // long contexts: up to 128 splits, merged once (model.rs:436-438),
@@ -502,6 +514,19 @@ static hipError_t timed_step(frn_ctx* c, bool with_logits) {
     c->t_calls[c->ev_cat[i]] += 1;
   }
   return hipSuccess;
+}
+
+// Short-context split counts that get their own step graphs: every count a
+// step within max_ctx can have (at most 16, up to ATTENTION_LONG_FROM).
+static uint32_t exact_forms(const frn_ctx* c) {
+  const uint32_t t = std::min<uint32_t>(c->cfg.max_ctx, ATTENTION_LONG_FROM);
+  return std::min<uint32_t>((t + ATTENTION_CHUNK - 1) / ATTENTION_CHUNK, ATTENTION_MAX_SPLITS);
+}
+// The exact-split graph index + 1 for a step over T positions, 0 for none.
+static uint32_t exact_splits(const frn_ctx* c, uint32_t T) {
+  if (T > ATTENTION_LONG_FROM) return 0;
+  const uint32_t n = (T + ATTENTION_CHUNK - 1) / ATTENTION_CHUNK;
+  return n <= exact_forms(c) && c->g_exact[n - 1] ? n : 0;
 }
 
 static frn_status capture(frn_ctx* c, bool with_logits, hipGraph_t* graph, hipGraphExec_t* exec,
@@ -743,13 +768,22 @@ extern "C" frn_status frn_finalize(frn_ctx* c) {
       if ((st = capture(c, true, &c->graph_multi[lng], &c->g_multi[lng], GREEDY_MULTI))) return st;
     }
     c->rec_long = false;
+    // decode steps whose attention grid is exactly their splits
+    for (uint32_t n = 1; n <= exact_forms(c); ++n) {
+      c->rec_splits = n;
+      if ((st = capture(c, true, &c->graph_exact[n - 1], &c->g_exact[n - 1]))) break;
+      if ((st = capture(c, true, &c->graph_exact_multi[n - 1], &c->g_exact_multi[n - 1], GREEDY_MULTI))) break;
+    }
+    c->rec_splits = 0;
+    if (st) return st;
   }
   c->finalized = true;
   return FRN_OK;
 }
 
 // Run one position with token `tok` (already validated); with_logits picks
-// the graph that ends in lm_head + argmax.  on_device: the token is the
+// the graph that ends in lm_head + argmax (the exact-split graph of the
+// step's position where there is one).  on_device: the token is the
 // previous step's argmax, already in StepState::tok.
 static frn_status run_step(frn_ctx* c, uint32_t tok, bool with_logits, bool on_device = false) {
   if (!on_device && tok != c->last_next) {
@@ -765,7 +799,9 @@ static frn_status run_step(frn_ctx* c, uint32_t tok, bool with_logits, bool on_d
     Tick tk{c, false};
     HIP_TRY(record_step(c, with_logits, tk), "eager step");
   } else {
-    HIP_TRY(hipGraphLaunch(with_logits ? c->g_step[c->rec_long] : c->g_prefill[c->rec_long], c->stream),
+    const uint32_t n = with_logits ? exact_splits(c, c->len + 1) : 0u;
+    HIP_TRY(hipGraphLaunch(n ? c->g_exact[n - 1] : with_logits ? c->g_step[c->rec_long] : c->g_prefill[c->rec_long],
+                           c->stream),
             "hipGraphLaunch");
   }
   c->len += 1;
@@ -980,7 +1016,9 @@ extern "C" frn_status frn_decode_greedy(frn_ctx* c, uint32_t id, uint32_t n, con
       if (done + i > 0 && b - i >= GREEDY_MULTI && same_form && !c->timing && !c->step_timing &&
           !(c->cfg.flags & FRN_FLAG_EAGER)) {
         c->rec_long = c->len + 1 > ATTENTION_LONG_FROM;
-        HIP_TRY(hipGraphLaunch(c->g_multi[c->rec_long], c->stream), "hipGraphLaunch");
+        const uint32_t n = exact_splits(c, c->len + 1);
+        const bool exact = n && n == exact_splits(c, c->len + GREEDY_MULTI);
+        HIP_TRY(hipGraphLaunch(exact ? c->g_exact_multi[n - 1] : c->g_multi[c->rec_long], c->stream), "hipGraphLaunch");
         c->len += GREEDY_MULTI;
         c->last_next = 0xFFFFFFFFu;
         i += GREEDY_MULTI;

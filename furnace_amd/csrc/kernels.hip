@@ -731,7 +731,7 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
                                                    float* __restrict__ kc, float* __restrict__ vc, uint32_t nh,
                                                    uint32_t nkv, uint32_t max_splits, uint32_t max_ctx, float scale,
                                                    float* __restrict__ part, const StepState* st, uint32_t cap,
-                                                   uint32_t gq) {
+                                                   uint32_t gq, uint32_t pre_all) {
   constexpr int C = ATT_CHUNK, TPP = 256 / C, DPT = HD / TPP, PARTS = 256 / HD, HALF = HD / 2, NP = C / PARTS;
   constexpr int RR = (GQ * HALF + HALF + 255) / 256;  // rotation rounds per thread
   // global loads: thread t moves float4 column lc of rows lr + RPI*i, so a
@@ -756,11 +756,13 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
   // the read of st->pos: the first sub-tile's K/V rows as if the split
   // were 64 positions (it is, up to 1024 positions; rows at or past the
   // position are masked or replaced below), and the rotation's q/k inputs.
-  // Only head group 0 streams the rows ahead: the blocks of splits past the
-  // position load them too before they know to exit, and the other groups'
-  // copies would multiply that waste.
+  // Only head group 0 streams the rows ahead when the grid holds splits
+  // past the position (their blocks load the rows too before they know to
+  // exit, and the other groups' copies would multiply that waste); a launch
+  // whose grid is exactly the step's splits (pre_all) streams them in every
+  // block.
   float4 kr[LD], vr[LD];
-  if (hz == 0) {
+  if (hz == 0 || pre_all) {
 #pragma unroll
     for (int i = 0; i < LD; ++i) {
       const uint32_t tp = split * C + lr + RPI * i;
@@ -805,7 +807,7 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
       vr[i] = *(const float4*)(vc + off);
     }
   };
-  if (len != C || hz != 0) load_tile(0);  // longer splits: the first sub-tile starts elsewhere
+  if (len != C || (hz != 0 && !pre_all)) load_tile(0);  // longer splits: the first sub-tile starts elsewhere
 #pragma unroll
   for (int r = 0; r < RR; ++r) {
     const int i = threadIdx.x + 256 * r;
@@ -964,18 +966,19 @@ hipError_t launch_attn_merge(const float* part, float* out, uint32_t nh, uint32_
 template <int HD, int GQ>
 static void att_go(dim3 grid, hipStream_t s, const float* q, const float* k, const float* v, const float* cs,
                    float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms, uint32_t max_ctx, float scale,
-                   float* part, const StepState* st, uint32_t cap, uint32_t gq) {
+                   float* part, const StepState* st, uint32_t cap, uint32_t gq, uint32_t pre_all) {
   hipLaunchKernelGGL((k_attention<HD, GQ>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale,
-                     part, st, cap, gq);
+                     part, st, cap, gq, pre_all);
 }
 
 template <int HD>
 static hipError_t att_gq(uint32_t hpb, dim3 grid, hipStream_t s, const float* q, const float* k, const float* v,
                          const float* cs, float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms,
-                         uint32_t max_ctx, float scale, float* part, const StepState* st, uint32_t cap, uint32_t gq) {
+                         uint32_t max_ctx, float scale, float* part, const StepState* st, uint32_t cap, uint32_t gq,
+                         uint32_t pre_all) {
   switch (hpb) {
 #define FRN_ATT_GQ(n) \
-  case n: att_go<HD, n>(grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st, cap, gq); break;
+  case n: att_go<HD, n>(grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st, cap, gq, pre_all); break;
     FRN_ATT_GQ(1) FRN_ATT_GQ(2) FRN_ATT_GQ(3) FRN_ATT_GQ(4) FRN_ATT_GQ(5) FRN_ATT_GQ(6) FRN_ATT_GQ(7) FRN_ATT_GQ(8)
 #undef FRN_ATT_GQ
     default: return hipErrorInvalidValue;
@@ -1006,13 +1009,16 @@ bool attention_supported(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_di
 
 hipError_t launch_attention(const float* q, const float* k, const float* v, const float* cs, float* kc, float* vc,
                             uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t max_ctx, float scale, float* part,
-                            const StepState* st, uint32_t cap, hipStream_t s) {
+                            const StepState* st, uint32_t cap, uint32_t live, hipStream_t s) {
   if (!attention_supported(nh, nkv, hd) || (cap != ATTENTION_MAX_SPLITS && cap != ATTENTION_MAX_SPLITS_LONG))
     return hipErrorInvalidValue;
   const uint32_t ms = attention_splits(max_ctx, cap), gq = nh / nkv, hpb = attention_heads_per_block(gq, cap);
-  dim3 grid(nkv, ms, (gq + hpb - 1) / hpb);
-  if (hd == 128) return att_gq<128>(hpb, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st, cap, gq);
-  return att_gq<64>(hpb, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st, cap, gq);
+  if (live && (cap != ATTENTION_MAX_SPLITS || live > ms)) return hipErrorInvalidValue;
+  dim3 grid(nkv, live ? live : ms, (gq + hpb - 1) / hpb);
+  const uint32_t pre = live ? 1u : 0u;
+  if (hd == 128)
+    return att_gq<128>(hpb, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st, cap, gq, pre);
+  return att_gq<64>(hpb, grid, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale, part, st, cap, gq, pre);
 }
 
 // ---- step bookkeeping and argmax (generate.rs:69-77) ------------------------

@@ -74,11 +74,14 @@ constexpr uint32_t ATTENTION_LONG_FROM = 1024;
 // cos | sin row), KV-cache append and split-sequence GQA attention in one
 // launch, with at most `cap` splits;
 // writes the per-split partials that a GEMV_RESID_ATT launch (cap 16) or
-// launch_attn_merge (cap 128) merges (layout in GemvArgs).
+// launch_attn_merge (cap 128) merges (layout in GemvArgs).  live > 0 (cap
+// 16 only): the launch serves only steps with exactly `live` splits (T in
+// (64 (live - 1), 64 live]); its grid holds those splits alone and every
+// block streams its K/V rows before it reads the step position.
 hipError_t launch_attention(const float* q, const float* k, const float* v, const float* rope_cur, float* k_cache,
                             float* v_cache, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                             uint32_t max_ctx, float scale, float* part, const StepState* st, uint32_t cap,
-                            hipStream_t s);
+                            uint32_t live, hipStream_t s);
 // The long-context merge: out[h][d] = sum_s e^(m_s - M) o_s[d] / sum_s
 // e^(m_s - M) l_s over the step's splits, one block per query head.
 hipError_t launch_attn_merge(const float* part, float* out, uint32_t n_heads, uint32_t head_dim, uint32_t max_ctx,

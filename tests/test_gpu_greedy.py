@@ -75,3 +75,31 @@ def test_greedy_stop_id_rolls_back(hip, tmpdir_models):
         tok = m.decode(tok)
         assert tok == ref[i], i
     m.close()
+
+
+def test_exact_split_graphs_across_split_boundaries(hip, tmpdir_models):
+    """Below 1024 positions each decode step replays the graph whose
+    attention grid is exactly its 64-position splits (four-step graphs only
+    where the four steps share the count).  150 steps from a 50-token prompt
+    cross the 64 and 128 boundaries at every offset of the four-step
+    groups; the ids and logits equal the eager steps' (one grid of all
+    splits) and the oracle's (model.rs:371-438)."""
+    from oracle import oracle as orc
+    path = os.path.join(tmpdir_models, "greedy.gguf")
+    if not os.path.exists(path):
+        fa.synth_write(path, seed=23, **SPEC)
+    prompt = np.random.default_rng(17).integers(0, SPEC["vocab"], 50).astype(np.uint32)
+    n = 150
+    ref = orc.Model(path)
+    ref_ids, _, ref_logits = ref.generate_greedy(prompt, n + 1, 256, stop_ids=[])
+    ref.close()
+    runs = []
+    for eager in (False, True):
+        m = fa.Model(path, max_ctx=256, eager=eager)
+        first = m.prefill(prompt)
+        ids = [first] + m.decode_greedy(first, n)
+        runs.append((ids, m.logits()))
+        m.close()
+    assert runs[0][0] == runs[1][0] == ref_ids
+    assert np.max(np.abs(runs[0][1] - runs[1][1])) <= 1e-3
+    assert np.max(np.abs(runs[0][1] - ref_logits)) <= 1e-3
