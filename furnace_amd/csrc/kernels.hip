@@ -492,14 +492,18 @@ __global__ __launch_bounds__(NT, 512 / NT) void k_gemv(GemvArgs a) {
 }
 
 // LDS of a launch: x as f32, then the int8 form's 4 planes of `in` bytes
-// (in <= 4096), or the f32 form's in/16 chunk sums after x, padded for
-// in <= 10240.
+// (in <= 4096), or the f32 form's in/16 chunk sums after x, with room for
+// the padded layout.
 size_t gemv_lds_bytes(uint32_t in, bool) {
   if (in <= 4096) return (size_t)in * 8 + in / 4;
   return (size_t)xf_padded_floats(in) * 4 + in / 4;  // 8-wave blocks: padded f32 form
 }
-// threads per block of a launch with input length in
-static uint32_t gemv_threads(uint32_t in) { return in <= 4096 ? 256u : 512u; }
+// Threads per block of a launch with input length in and first-segment
+// format t: 8 waves for the K-quants' long inputs (the padded f32 form), 4
+// otherwise (the Q8_0 f32 form measured faster at 4 waves: 0.5B decode
+// 1353 tokens/s with 8-wave down blocks against 1484 with 4).
+__host__ __device__ constexpr bool gemv_wide(uint32_t in, uint32_t t) { return in > 4096 && (t == T_Q4_K || t == T_Q6_K); }
+static uint32_t gemv_threads(uint32_t in, uint32_t t) { return gemv_wide(in, t) ? 512u : 256u; }
 
 
 // Lanes per row: the choice in {16, 32, 64} with the shortest critical
@@ -508,9 +512,9 @@ static uint32_t gemv_threads(uint32_t in) { return in <= 4096 ? 256u : 512u; }
 // stage x).  E.g. the 1.5B SwiGLU pair (8960 rows of 48 items, 2 items per
 // lane and step): 16 lanes -> 2240 units of 2 steps on 2048 waves, 4
 // steps; 32 lanes -> 4480 units of 1 step, 3 steps.
-static uint32_t max_blocks(uint32_t in);
+static uint32_t max_blocks(uint32_t in, uint32_t t);
 static int lanes_per_row(uint32_t total_rows, uint32_t in, uint32_t type, int mode, int n_items) {
-  const uint32_t nw = gemv_threads(in) / 64, cap_waves = nw * max_blocks(in);
+  const uint32_t nw = gemv_threads(in, type) / 64, cap_waves = nw * max_blocks(in, type);
   int best_l = 16;
   uint64_t best = ~0ull;
   for (int l = 16; l <= 64; l *= 2) {
@@ -526,11 +530,11 @@ static int lanes_per_row(uint32_t total_rows, uint32_t in, uint32_t type, int mo
   return best_l;
 }
 
-// Grid cap: 2 blocks (8 waves) per CU for in <= 4096, one 8-wave block per
-// CU above.  (A cap of 4 per CU, which LDS would allow for small in,
-// measured no faster: the kernels are VALU-bound, not short of waves.)
-static uint32_t max_blocks(uint32_t in) {
-  if (gemv_threads(in) == 512) return 256;
+// Grid cap: 2 blocks (8 waves) per CU for in <= 4096, one block per CU
+// above.  (A cap of 4 per CU, which LDS would allow for small in, measured
+// no faster: the kernels are VALU-bound, not short of waves.)
+static uint32_t max_blocks(uint32_t in, uint32_t t) {
+  if (gemv_threads(in, t) == 512) return 256;
   const size_t lds = gemv_lds_bytes(in, false);
   return lds > 80 * 1024 ? 256 : lds > 40 * 1024 ? 512 : GEMV_MAX_GRID;
 }
@@ -538,7 +542,8 @@ static uint32_t max_blocks(uint32_t in) {
 // Blocks per segment in proportion to its units of 64 / LPR rows; each
 // block runs 4 wave workers; at most as many blocks as are resident at once.
 static uint32_t plan_blocks(GemvArgs& a, uint32_t rows_per_unit) {
-  uint32_t want[3], total = 0, cap = max_blocks(a.in), nw = gemv_threads(a.in) / 64;
+  const uint32_t t = a.seg[0].type;
+  uint32_t want[3], total = 0, cap = max_blocks(a.in, t), nw = gemv_threads(a.in, t) / 64;
   for (int i = 0; i < a.n_seg; ++i) {
     uint32_t units = (a.seg[i].rows + rows_per_unit - 1) / rows_per_unit;
     want[i] = (units + nw - 1) / nw;
@@ -557,8 +562,8 @@ static uint32_t plan_blocks(GemvArgs& a, uint32_t rows_per_unit) {
 
 uint32_t gemv_blocks(uint32_t type, uint32_t rows, uint32_t in) {
   int lpr = lanes_per_row(rows, in, type, GEMV_STORE, items_per_row(type, in, ((in / 32) % 2) == 0));
-  const uint32_t nw = gemv_threads(in) / 64;
-  uint32_t units = (rows + 64 / lpr - 1) / (64 / lpr), want = (units + nw - 1) / nw, cap = max_blocks(in);
+  const uint32_t nw = gemv_threads(in, type) / 64;
+  uint32_t units = (rows + 64 / lpr - 1) / (64 / lpr), want = (units + nw - 1) / nw, cap = max_blocks(in, type);
   return want < cap ? want : cap;
 }
 
@@ -574,16 +579,20 @@ static hipError_t go(GemvArgs a, hipStream_t s, uint32_t* nblocks) {
 
 // in <= 4096 (the hidden-size inputs, with or without rmsnorm; 4-wave
 // blocks) or, without rmsnorm and only for STORE/RESID, in <= 20480 (the
-// FFN down projection; 8-wave blocks, NX 3 up to 12288, NX 5 above).
+// FFN down projection; K-quants in 8-wave blocks, NX 3 up to 12288, NX 5
+// above; other formats in 4-wave blocks, NX 5 up to 10240, NX 10 above).
 template <uint32_t T0, uint32_t T1, int MODE, int LPR>
 static hipError_t pick_nx(const GemvArgs& a, hipStream_t s, uint32_t* nb) {
   const int n_items = items_per_row(T0, a.in, ((a.in / 32) % 2) == 0);
   const bool one = n_items <= LPR * gemv_bi(T0, MODE);  // one step per unit
   if (a.in <= 2048) return one ? go<T0, T1, LPR, MODE, 1, true>(a, s, nb) : go<T0, T1, LPR, MODE, 1, false>(a, s, nb);
   if (a.in <= 4096) return one ? go<T0, T1, LPR, MODE, 2, true>(a, s, nb) : go<T0, T1, LPR, MODE, 2, false>(a, s, nb);
-  if constexpr (MODE == GEMV_STORE || MODE == GEMV_RESID) {
+  if constexpr ((MODE == GEMV_STORE || MODE == GEMV_RESID) && (T0 == T_Q4_K || T0 == T_Q6_K)) {
     if (a.norm_w == nullptr && a.in <= 12288) return go<T0, T1, LPR, MODE, 3, false, 512>(a, s, nb);
     if (a.norm_w == nullptr && a.in <= 20480) return go<T0, T1, LPR, MODE, 5, false, 512>(a, s, nb);
+  } else if constexpr (MODE == GEMV_STORE || MODE == GEMV_RESID) {
+    if (a.norm_w == nullptr && a.in <= 10240) return go<T0, T1, LPR, MODE, 5, false>(a, s, nb);
+    if (a.norm_w == nullptr && a.in <= 20480) return go<T0, T1, LPR, MODE, 10, false>(a, s, nb);
   }
   return hipErrorInvalidValue;
 }
@@ -653,16 +662,23 @@ hipError_t launch_gemv(GemvArgs a, GemvMode mode, hipStream_t s, uint32_t* nb) {
   return hipErrorInvalidValue;
 }
 
-// Only the in > 4096 kernels (8-wave blocks, NX 3 and 5) can use more than
-// the default 64 KiB of dynamic LDS.
+// Only the in > 4096 kernels can use more than the default 64 KiB of
+// dynamic LDS.
 template <uint32_t T0, uint32_t T1, int LPR>
 static hipError_t prep_one(int bytes) {
   hipError_t e;
   const auto attr = hipFuncAttributeMaxDynamicSharedMemorySize;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 3, false, 512>, attr, bytes))) return e;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 5, false, 512>, attr, bytes))) return e;
-  if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 3, false, 512>, attr, bytes))) return e;
-  return hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 5, false, 512>, attr, bytes);
+  if constexpr (T0 == T_Q4_K || T0 == T_Q6_K) {
+    if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 3, false, 512>, attr, bytes))) return e;
+    if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 5, false, 512>, attr, bytes))) return e;
+    if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 3, false, 512>, attr, bytes))) return e;
+    return hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 5, false, 512>, attr, bytes);
+  } else {
+    if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 5, false, 256>, attr, bytes))) return e;
+    if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_STORE, 10, false, 256>, attr, bytes))) return e;
+    if ((e = hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 5, false, 256>, attr, bytes))) return e;
+    return hipFuncSetAttribute((const void*)k_gemv<T0, T1, LPR, GEMV_RESID, 10, false, 256>, attr, bytes);
+  }
 }
 
 template <uint32_t T0, uint32_t T1>

@@ -13,8 +13,11 @@
 //                     hi.lo, lo.hi); epilogues: store + bias, residual add,
 //                     SwiGLU of two weights into split planes
 //  - k_rope_kv_rows   RoPE of q and k rows at their positions, KV append
-//  - k_attn_rows_mfma causal GQA attention of 32 query rows of one head over
-//                     the cache on v_mfma_f32_32x32x2f32 (S^T = K Q^T, then
+//  - k_kv_split       a layer's K and V as bf16 hi + lo planes (V transposed)
+//  - k_attn_rows_mfma causal GQA attention of 128 query rows of one head per
+//                     block (one wave per 32 rows) over the cache, key tiles
+//                     shared through LDS, on split-operand
+//                     v_mfma_f32_32x32x16_bf16 (S^T = K Q^T, then
 //                     O^T += V^T P^T), online softmax over 32-key tiles
 //
 // The split products carry 16+ significant bits per operand into f32
