@@ -939,18 +939,30 @@ size_t attention_part_floats(uint32_t nh, uint32_t hd, uint32_t max_ctx) {
   return (size_t)nh * attention_splits(max_ctx, ATTENTION_MAX_SPLITS_LONG) * (hd + 2);
 }
 
-// Long-context merge of the splits of one query head (block h, thread d):
-// the split maxima and sums go through LDS, then each thread combines its
-// dimension over the splits (their loads independent of each other).
+// Long-context merge of the splits of one query head (block h): thread
+// (d, q) of the 4 HD threads holds dimension d of the splits q, q + 4, ...
+// Its o loads go out first, over all ms splits of the buffer (in bounds;
+// those past the step's count are not used), so they do not wait for the
+// position; the splits' maxima and sums go through LDS; each thread sums
+// its splits with the weights e^(m_s - M), and the four partial sums of a
+// dimension are added in q order.
 template <int HD>
-__global__ __launch_bounds__(HD) void k_attn_merge(const float* __restrict__ part, float* __restrict__ out,
-                                                   uint32_t ms, const StepState* st) {
+__global__ __launch_bounds__(4 * HD) void k_attn_merge(const float* __restrict__ part, float* __restrict__ out,
+                                                       uint32_t ms, const StepState* st) {
+  constexpr int NQ = 4, PER = ATTENTION_MAX_SPLITS_LONG / NQ;
   __shared__ float msl[2 * ATTENTION_MAX_SPLITS_LONG];
-  const uint32_t h = blockIdx.x, d = threadIdx.x;
+  __shared__ float po[NQ][HD], pl[NQ];
+  const uint32_t h = blockIdx.x, d = threadIdx.x % HD, q = threadIdx.x / HD;
+  const float* base = part + (size_t)h * ms * (HD + 2);
+  float ov[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t sp = q + NQ * i;
+    ov[i] = sp < ms ? base[(size_t)sp * (HD + 2) + d] : 0.f;
+  }
   const uint32_t T = st->pos + 1, len = attention_split_len(T, ATTENTION_MAX_SPLITS_LONG);
   const uint32_t ns = (T + len - 1) / len;
-  const float* base = part + (size_t)h * ms * (HD + 2);
-  for (uint32_t sp = d; sp < ns; sp += HD) {
+  for (uint32_t sp = threadIdx.x; sp < ns; sp += NQ * HD) {
     msl[2 * sp] = base[(size_t)sp * (HD + 2) + HD];
     msl[2 * sp + 1] = base[(size_t)sp * (HD + 2) + HD + 1];
   }
@@ -958,22 +970,36 @@ __global__ __launch_bounds__(HD) void k_attn_merge(const float* __restrict__ par
   float M = -INFINITY;
   for (uint32_t sp = 0; sp < ns; ++sp) M = fmaxf(M, msl[2 * sp]);
   float o = 0.f, L = 0.f;
-#pragma unroll 8
-  for (uint32_t sp = 0; sp < ns; ++sp) {
-    const float e = expf(msl[2 * sp] - M);  // model.rs:371-438, evaluated split-wise
-    L += e * msl[2 * sp + 1];
-    o += e * base[(size_t)sp * (HD + 2) + d];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const uint32_t sp = q + NQ * i;
+    if (sp < ns) {
+      const float e = expf(msl[2 * sp] - M);  // model.rs:371-438, evaluated split-wise
+      L += e * msl[2 * sp + 1];
+      o += e * ov[i];
+    }
   }
-  out[(size_t)h * HD + d] = L > 0.f ? o / L : 0.f;
+  po[q][d] = o;
+  if (d == 0) pl[q] = L;
+  __syncthreads();
+  if (q == 0) {
+    float O = po[0][d], Lt = pl[0];
+#pragma unroll
+    for (int k = 1; k < NQ; ++k) {
+      O += po[k][d];
+      Lt += pl[k];
+    }
+    out[(size_t)h * HD + d] = Lt > 0.f ? O / Lt : 0.f;
+  }
 }
 
 hipError_t launch_attn_merge(const float* part, float* out, uint32_t nh, uint32_t hd, uint32_t max_ctx,
                              const StepState* st, hipStream_t s) {
   const uint32_t ms = attention_splits(max_ctx, ATTENTION_MAX_SPLITS_LONG);
   if (hd == 128)
-    hipLaunchKernelGGL(k_attn_merge<128>, dim3(nh), dim3(128), 0, s, part, out, ms, st);
+    hipLaunchKernelGGL(k_attn_merge<128>, dim3(nh), dim3(4 * 128), 0, s, part, out, ms, st);
   else if (hd == 64)
-    hipLaunchKernelGGL(k_attn_merge<64>, dim3(nh), dim3(64), 0, s, part, out, ms, st);
+    hipLaunchKernelGGL(k_attn_merge<64>, dim3(nh), dim3(4 * 64), 0, s, part, out, ms, st);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
