@@ -104,6 +104,7 @@ struct frn_ctx {
   float *pf_x = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
   // the GEMM operands as bf16 hi + lo planes: rmsnorm'd x, attention rows, SwiGLU activation
   uint16_t *pf_xs = nullptr, *pf_att = nullptr, *pf_act = nullptr;
+  uint16_t* pf_xg = nullptr;  // group sums of a Q4_K GEMM's input planes (launch_group_sums)
   uint16_t* pf_kvs = nullptr;  // a layer's K and V as the prefill attention's bf16 planes (max_ctx keys)
   uint32_t* pf_ids = nullptr;
   uint32_t len = 0;           // host view of KvCache::len
@@ -165,7 +166,7 @@ static void free_ctx(frn_ctx* c) {
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->st_ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.terms, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_kvs, c->pf_ids};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.terms, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_kvs, c->pf_ids, c->pf_xg};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -216,6 +217,7 @@ static hipError_t alloc_prefill(frn_ctx* x) {
       (e = dmalloc(&x->pf_k, P * kvd * 4)) || (e = dmalloc(&x->pf_v, P * kvd * 4)) ||
       (e = dmalloc(&x->pf_xs, P * c.hidden * 4)) || (e = dmalloc(&x->pf_att, P * qd * 4)) ||
       (e = dmalloc(&x->pf_act, P * c.ffn * 4)) || (e = dmalloc(&x->pf_ids, P * 4)) ||
+      (e = dmalloc(&x->pf_xg, P * std::max<size_t>(std::max<size_t>(c.hidden, qd), c.ffn) / 32 * 4)) ||
       (e = dmalloc(&x->pf_kvs, kv_split_elems(c.max_ctx, (uint32_t)kvd) * 2)))
     return e;
   return hipSuccess;
@@ -849,11 +851,19 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
       return e;
     // the planes of an operand [m][K]: hi first, lo after
     auto lo_of = [&](uint16_t* hi, uint32_t K) { return hi + (size_t)m * K; };
+    // the group sums a Q4_K weight reads beside its input planes
+    auto group_sums = [&](GemmArgs& ga, uint16_t* a, uint32_t K) {
+      ga.x_hi = c->pf_xg;
+      ga.x_lo = c->pf_xg + (size_t)m * (K / 32);
+      return launch_group_sums(a, lo_of(a, K), m, K, c->pf_xg, c->pf_xg + (size_t)m * (K / 32), s);
+    };
     auto gemm = [&](const DevTensor* w, const DevTensor* w2, uint16_t* a, uint32_t K, const float* bias, float* out,
                     uint16_t* o_planes, uint32_t ldo, GemmMode mode) {
       GemmArgs ga{};
       ga.a_hi = a;
       ga.a_lo = lo_of(a, K);
+      if (w->type == T_Q4_K)
+        if (hipError_t r = group_sums(ga, a, K)) return r;
       ga.w = w->ptr;
       ga.w2 = w2 ? w2->ptr : nullptr;
       ga.type = w->type;
@@ -875,11 +885,16 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
       float* o[3] = {c->pf_q, c->pf_k, c->pf_v};
       const uint32_t ld[3] = {QD, KVD, KVD};
       bool done[3] = {false, false, false};
+      GemmArgs sums{};  // computed once for the launches that read them
+      if (w[0]->type == T_Q4_K || w[1]->type == T_Q4_K || w[2]->type == T_Q4_K)
+        if (hipError_t r = group_sums(sums, c->pf_xs, H)) return r;
       for (int i = 0; i < 3; ++i) {
         if (done[i]) continue;
         GemmArgs ga{};
         ga.a_hi = c->pf_xs;
         ga.a_lo = lo_of(c->pf_xs, H);
+        ga.x_hi = sums.x_hi;
+        ga.x_lo = sums.x_lo;
         ga.w = w[i]->ptr;
         ga.type = w[i]->type;
         ga.row_bytes = (uint32_t)type_row_bytes(w[i]->type, w[i]->in);

@@ -115,10 +115,13 @@ enum GemmMode : int { GEMM_STORE = 0, GEMM_RESID = 1, GEMM_SWIGLU = 2 };
 // planes, a_hi + a_lo (row stride K; launch_rows_split, the attention rows
 // and the SwiGLU epilogue write that form).  STORE: out = C (+ bias);
 // RESID: out += C; SWIGLU: silu(C(w)) * C(w2), split into the planes
-// o_hi / o_lo (row stride ldo).
+// o_hi / o_lo (row stride ldo).  Q4_K weights also read the sums of A's
+// 32-value groups, x_hi + x_lo (launch_group_sums).
 struct GemmArgs {
   const uint16_t* a_hi;  // [P][K] bf16
   const uint16_t* a_lo;  // [P][K] bf16
+  const uint16_t* x_hi;  // Q4_K: [P][K / 32] bf16, group sums of a_hi + a_lo
+  const uint16_t* x_lo;
   const uint8_t* w;      // [N] rows of row_bytes raw blocks
   const uint8_t* w2;     // SWIGLU: the up matrix
   uint32_t type, row_bytes;
@@ -146,6 +149,10 @@ hipError_t gemm_prepare();
 // nw is given -- split into the bf16 planes hi + lo that the GEMM reads.
 hipError_t launch_rows_split(const float* x, uint32_t rows, uint32_t cols, const float* nw, float eps, uint16_t* hi,
                              uint16_t* lo, hipStream_t s);
+// Sums of the 32-value groups of rows [rows][cols] given as bf16 planes
+// hi + lo, each sum split into the planes xh + xl ([rows][cols / 32]).
+hipError_t launch_group_sums(const uint16_t* hi, const uint16_t* lo, uint32_t rows, uint32_t cols, uint16_t* xh,
+                             uint16_t* xl, hipStream_t s);
 hipError_t launch_embed_rows(const uint8_t* table, uint32_t type, uint32_t hidden, uint32_t row_bytes,
                              const uint32_t* ids, uint32_t n, float* x, hipStream_t s);
 // RoPE of n q rows (in place) and k rows (into the cache) at positions

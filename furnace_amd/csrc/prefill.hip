@@ -5,13 +5,19 @@
 //  - k_embed_rows     embedding rows of the block's token ids
 //  - k_rows_split     rows of x, rmsnorm'd when a gain is given, split into
 //                     the bf16 planes x = hi + lo the GEMMs read
-//  - k_gemm_b3        C = A . W^T with W in its raw GGUF blocks: each
-//                     k-step dequantizes a weight tile (f32, the formulas
-//                     of the dequant kernel with fused products), splits it into
-//                     bf16 hi + lo in LDS beside the A planes, and runs
-//                     three v_mfma_f32_32x32x16_bf16 per tile pair (hi.hi,
-//                     hi.lo, lo.hi); epilogues: store + bias, residual add,
-//                     SwiGLU of two weights into split planes
+//  - k_group_sums     sums of the 32-value groups of split rows (the Q4_K
+//                     GEMMs' offset term)
+//  - k_gemm_b3        C = A . W^T with W in its raw GGUF blocks: each wave
+//                     decodes its weight rows straight into MFMA operands.
+//                     Q4_K: the exact quants as bf16, two
+//                     v_mfma_f32_32x32x16_bf16 per operand pair (q.x_hi,
+//                     q.x_lo) into a per-group product scaled by d sc, and
+//                     the groups' -dmin m offsets applied per 16 groups with
+//                     the group sums; the other formats: the dequantized
+//                     weight (f32, the dequant kernel's formulas with fused
+//                     products) split into bf16 hi + lo, three MFMAs per
+//                     pair (hi.hi, hi.lo, lo.hi).  Epilogues: store + bias,
+//                     residual add, SwiGLU of two weights into split planes
 //  - k_rope_kv_rows   RoPE of q and k rows at their positions, KV append
 //  - k_kv_split       a layer's K and V as bf16 hi + lo planes (V transposed)
 //  - k_attn_rows_mfma causal GQA attention of 128 query rows of one head per
@@ -21,8 +27,8 @@
 //                     O^T += V^T P^T), online softmax over 32-key tiles
 //
 // The split products carry 16+ significant bits per operand into f32
-// accumulators: the GEMM differs from the CPU path by the order of its
-// sums and a relative error below ~2^-15 per product.
+// accumulators (Q4_K quants exactly): the GEMM differs from the CPU path by
+// the order of its sums and a relative error below ~2^-15 per product.
 #include <stdlib.h>
 
 #include <type_traits>
@@ -120,6 +126,36 @@ hipError_t launch_rows_split(const float* x, uint32_t rows, uint32_t cols, const
                              uint16_t* lo, hipStream_t s) {
   if (cols % 8) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_rows_split, dim3(rows), dim3(256), 0, s, x, cols, nw, eps, hi, lo);
+  return hipGetLastError();
+}
+
+// One thread per 32-value group of a row: the sum of its values hi + lo in
+// index order (each hi + lo is exact in f32), split into bf16 hi + lo.
+__global__ __launch_bounds__(256) void k_group_sums(const uint16_t* __restrict__ hi, const uint16_t* __restrict__ lo,
+                                                    uint32_t cols, uint16_t* __restrict__ xh,
+                                                    uint16_t* __restrict__ xl) {
+  const uint32_t r = blockIdx.y, ng = cols / 32, gi = blockIdx.x * 256 + threadIdx.x;
+  if (gi >= ng) return;
+  const uint4* ph = (const uint4*)(hi + (size_t)r * cols + 32 * gi);
+  const uint4* pl = (const uint4*)(lo + (size_t)r * cols + 32 * gi);
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint4 a = ph[c], b = pl[c];
+    const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {  // value 2e in the low half, 2e + 1 in the high half
+      sum += __uint_as_float(wa[e] << 16) + __uint_as_float(wb[e] << 16);
+      sum += __uint_as_float(wa[e] & 0xFFFF0000u) + __uint_as_float(wb[e] & 0xFFFF0000u);
+    }
+  }
+  split1(sum, xh[(size_t)r * ng + gi], xl[(size_t)r * ng + gi]);
+}
+
+hipError_t launch_group_sums(const uint16_t* hi, const uint16_t* lo, uint32_t rows, uint32_t cols, uint16_t* xh,
+                             uint16_t* xl, hipStream_t s) {
+  if (cols % 32 || rows == 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_group_sums, dim3((cols / 32 + 255) / 256, rows), dim3(256), 0, s, hi, lo, cols, xh, xl);
   return hipGetLastError();
 }
 
@@ -279,9 +315,11 @@ struct Deq8<T_F32> {
 // matrix, k-steps of 32.  The A planes of a k-step go through LDS (shared
 // by the 4 waves; double buffer, one barrier per k-step); each wave loads,
 // decodes and splits its own weight rows straight into MFMA operands, so
-// no weight value is decoded twice and the LDS carries only A.  Per k-step
-// a wave runs 2 x MT x NW x NJ x 3 v_mfma_f32_32x32x16_bf16 (hi.hi, hi.lo,
-// lo.hi; the lo.lo term is below 2^-14 of the product).  Lane l supplies
+// no weight value is decoded twice and the LDS carries only A (and, for
+// Q4_K, each wave's window of group offsets).  Per k-step a wave runs
+// 2 x MT x NW x NJ x 3 v_mfma_f32_32x32x16_bf16 (hi.hi, hi.lo, lo.hi; the
+// lo.lo term is below 2^-14 of the product), Q4_K 2 x MT x NW x NJ x 2
+// (+ 3 per 16 k-steps for the offsets).  Lane l supplies
 // A[l%32][8(l/32) .. +8] and B[8(l/32) .. +8][l%32]; register v of lane l
 // is C[8(v/4) + 4(l/32) + v%4][l%32] (layouts checked on gfx950).  The raw
 // weight bytes of k-step t + 2 and the A planes of k-step t + 1 are in
@@ -291,6 +329,12 @@ constexpr int BKP = 56;
 template <int MT>
 __host__ __device__ constexpr uint32_t gemm_lds_bytes() {
   return 2u * 2u * 32u * MT * BKP * 2u;  // 2 buffers x 2 planes x rows x padded row
+}
+// Q4_K: + each wave's window of group offsets, [32 rows][16 groups] f32
+// per weight tile
+template <uint32_t T, int MODE, int MT, int NJ>
+__host__ __device__ constexpr uint32_t gemm_lds_bytes_t() {
+  return gemm_lds_bytes<MT>() + (T == T_Q4_K ? 4u * (MODE == GEMM_SWIGLU ? 2u : 1u) * NJ * 512u * 4u : 0u);
 }
 
 template <uint32_t T, int MODE, int MT, int NJ>
@@ -346,8 +390,65 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   // (the memory pipeline, not the matrix cores, bounds this GEMM).  The
   // k order inside a k-step is permuted to match (MFMA half ks of lane
   // half h takes values 16h + 8ks .. +8, in A as in W).
+  f32x16 acc[MT][NW][NJ];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][w][j][v] = 0.f;
+
   constexpr bool QK = T == T_Q4_K;
   uint4 qhdr[2][NW][NJ], qraw[2][NW][NJ];
+  // Q4_K splits each 32-value group's dot product as quant.rs:101-106's
+  // terms: (d sc) * sum(q x) - (dmin m) * sum(x).  The quants q (0..15)
+  // are exact in bf16, so sum(q x) takes two MFMAs per operand pair
+  // (q.x_hi, q.x_lo) into a per-group product that is scaled by d sc into
+  // the accumulator.  The offsets -dmin m of 16 consecutive groups collect
+  // in LDS (the wave's [32 rows][16 groups] f32 window) and are applied as
+  // one more k = 16 product with the groups' sums of x (x_hi + x_lo, from
+  // launch_group_sums), split three ways like the other operands.
+  float* const mwin0 = (float*)(lds16 + 4 * A_PL);
+  auto mwin = [&](int w, int j) { return mwin0 + ((wave * NW + w) * NJ + j) * 512; };
+  const rsrc_t rxh = make_rsrc(QK ? g.x_hi : nullptr, QK ? g.P * nk * 2 : 0);
+  const rsrc_t rxl = make_rsrc(QK ? g.x_lo : nullptr, QK ? g.P * nk * 2 : 0);
+  // the offsets of window wi (groups 16 wi .. +16; `half`: only the first
+  // 8 exist) times the group sums, into the accumulators
+  auto offsets = [&](uint32_t wi, bool half) {
+    const int h = lane >> 5;
+    const bool live = !half || h == 0;
+    bf16x8 mh[NW][NJ], ml[NW][NJ];
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const float* mp = mwin(w, j) + 16 * col + 8 * h;
+        const float4 u = *(const float4*)mp, v = *(const float4*)(mp + 4);
+        float y[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = live ? y[e] : 0.f;
+        uint4 hi, lo;
+        split8(y, hi, lo);
+        mh[w][j] = __builtin_bit_cast(bf16x8, hi);
+        ml[w][j] = __builtin_bit_cast(bf16x8, lo);
+      }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const uint32_t r = r0 + 32 * i + col;
+      const uint32_t o = live && r < g.P ? 2 * (r * nk + 16 * wi + 8 * h) : BUF_INVALID;
+      const bf16x8 xh = __builtin_bit_cast(bf16x8, bl128(rxh, o)), xl = __builtin_bit_cast(bf16x8, bl128(rxl, o));
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          acc[i][w][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, mh[w][j], acc[i][w][j], 0, 0, 0);
+          acc[i][w][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, ml[w][j], acc[i][w][j], 0, 0, 0);
+          acc[i][w][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, mh[w][j], acc[i][w][j], 0, 0, 0);
+        }
+    }
+  };
   auto fetch_wq = [&](int s, uint32_t grp) {
     const uint32_t sb = (grp / 4) * 144u, qo = sb + 16u + 32u * (grp % 4) + (uint32_t)(2 * kh);
 #pragma unroll
@@ -422,16 +523,6 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
           pw[s][w][j][ks].load(rw[w], kt >= nk ? BUF_INVALID : w_off[j], 32 * kt + 16 * ks + kh);
   };
 
-  f32x16 acc[MT][NW][NJ];
-#pragma unroll
-  for (int i = 0; i < MT; ++i)
-#pragma unroll
-    for (int w = 0; w < NW; ++w)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][w][j][v] = 0.f;
-
   // k-step kt: LDS buffer kt & 1, weight register set kt & 1.  Two k-steps
   // per trip keep every buffer and set index a constant (a register array
   // indexed at run time would live in scratch memory).
@@ -468,28 +559,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
     // weight matrix); with two (SwiGLU) the second half's are read once
     // the first half's MFMAs are issued, so they reuse its registers
     constexpr bool A_EARLY = NW == 1 || MT <= 2;
-    read_a(0);
-    if constexpr (A_EARLY) read_a(1);
+    if constexpr (!QK) {
+      read_a(0);
+      if constexpr (A_EARLY) read_a(1);
+    }
     auto decode = [&](int ks) {
 #pragma unroll
       for (int w = 0; w < NW; ++w)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           float y[8];
-          if constexpr (QK) {  // quant.rs:93-109, sub-block kt % 8
-            const uint4 hd = qhdr[S][w][j], q = qraw[S][w][j];
-            const float d = f16_bits_to_f32(hd.x & 0xFFFFu), dmin = f16_bits_to_f32(hd.x >> 16);
-            uint32_t sc, m;
-            q4k_scale_min_regs(hd.y, hd.z, hd.w, (int)(kt % 8), sc, m);
-            const float dd = d * (float)sc, mm = dmin * (float)m;
-            const uint32_t n0 = ((ks ? q.z : q.x) >> (4 * H)) & 0x0F0F0F0Fu;
-            const uint32_t n1 = ((ks ? q.w : q.y) >> (4 * H)) & 0x0F0F0F0Fu;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              y[i] = fmaf(dd, byte_f(n0, i), -mm);
-              y[4 + i] = fmaf(dd, byte_f(n1, i), -mm);
-            }
-          } else if constexpr (Q6) {  // quant.rs:114-133, quarter K6 of half (kt / 4) % 2
+          if constexpr (Q6) {  // quant.rs:114-133, quarter K6 of half (kt / 4) % 2
             const uint32_t sh = (w_off[j] + (kt / 8) * 210u) & 3u;
             uint32_t lo4[4], hi4[4];
             realign16(q6l[S][w][j][K6 & 1].a, q6l[S][w][j][K6 & 1].x, sh, lo4);
@@ -532,15 +612,62 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
             acc[i][w][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[ks][i], bh[ks][w][j], acc[i][w][j], 0, 0, 0);
         }
     };
-    decode(0);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(0);
-    if constexpr (!A_EARLY) {
+    if constexpr (QK) {  // quant.rs:93-109, group kt % 8 of superblock kt / 8
+      bf16x8 bq[2][NW][NJ];
+      float dsc[NW][NJ];
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const uint4 hd = qhdr[S][w][j], q = qraw[S][w][j];
+          uint32_t sc, m;
+          q4k_scale_min_regs(hd.y, hd.z, hd.w, (int)(kt % 8), sc, m);
+          dsc[w][j] = f16_bits_to_f32(hd.x & 0xFFFFu) * (float)sc;
+          mwin(w, j)[16 * col + (kt & 15)] = -(f16_bits_to_f32(hd.x >> 16) * (float)m);
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const uint32_t n0 = ((ks ? q.z : q.x) >> (4 * H)) & 0x0F0F0F0Fu;
+            const uint32_t n1 = ((ks ? q.w : q.y) >> (4 * H)) & 0x0F0F0F0Fu;
+            const uint4 u = make_uint4(pk_bf16(byte_f(n0, 0), byte_f(n0, 1)), pk_bf16(byte_f(n0, 2), byte_f(n0, 3)),
+                                       pk_bf16(byte_f(n1, 0), byte_f(n1, 1)), pk_bf16(byte_f(n1, 2), byte_f(n1, 3)));
+            bq[ks][w][j] = __builtin_bit_cast(bf16x8, u);
+          }
+        }
+      // per token tile: the group's product in a fresh accumulator (four
+      // MFMAs), then scaled into the tile's accumulator.  The empty asm
+      // pins each scaling here, so that one product is live at a time.
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const uint16_t* ar = A(b, 0) + (32 * i + col) * BKP + 2 * kh;
+        const uint16_t* al_ = A(b, 1) + (32 * i + col) * BKP + 2 * kh;
+        const bf16x8 a0h = *(const bf16x8*)ar, a0l = *(const bf16x8*)al_;
+        const bf16x8 a1h = *(const bf16x8*)(ar + 8), a1l = *(const bf16x8*)(al_ + 8);
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            f32x16 t = {};
+            t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0h, bq[0][w][j], t, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0l, bq[0][w][j], t, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1h, bq[1][w][j], t, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1l, bq[1][w][j], t, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][w][j][v] = fmaf(dsc[w][j], t[v], acc[i][w][j][v]);
+            asm volatile("" : "+v"(acc[i][w][j]));
+          }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      decode(0);
       __builtin_amdgcn_sched_barrier(0);
-      read_a(1);
+      mma(0);
+      if constexpr (!A_EARLY) {
+        __builtin_amdgcn_sched_barrier(0);
+        read_a(1);
+      }
+      decode(1);
+      mma(1);
     }
-    decode(1);
-    mma(1);
     // weights two k-steps (Q4_K: two groups) ahead; past the end: no memory access
     if constexpr (QK) {
       if (H == 1) fetch_wq(S, (kt + 3) / 2);
@@ -558,6 +685,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
       }
     }
     __syncthreads();
+    // a full window of offsets (written before the barrier above)
+    if constexpr (QK && pc == 3) {
+      if ((kt & 15) == 15) offsets(kt / 16, false);
+    }
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -585,6 +716,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
       step(std::integral_constant<int, 2>{}, kt + 2);
       step(std::integral_constant<int, 3>{}, kt + 3);
     }
+    if (nk & 15) offsets(nk / 16, true);  // a row of 16 w + 8 groups
   } else if constexpr (Q6) {
     // eight k-steps (a superblock: its two halves) per trip
     for (uint32_t kt = 0; kt < nk; kt += 8) {
@@ -637,7 +769,8 @@ static hipError_t gemm_go_b3(const GemmArgs& g, hipStream_t s) {
   constexpr uint32_t lds = gemm_lds_bytes<MT>();
   if constexpr (MODE == GEMM_SWIGLU && MT == 4) {  // Q4_K only (gemm_go)
     if (g.type != T_Q4_K) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_gemm_b3<T_Q4_K, MODE, MT, NJ>), grid, dim3(256), lds, s, g);
+    hipLaunchKernelGGL((k_gemm_b3<T_Q4_K, MODE, MT, NJ>), grid, dim3(256), (gemm_lds_bytes_t<T_Q4_K, MODE, MT, NJ>()),
+                       s, g);
     return hipGetLastError();
   } else {
     return gemm_go_types<MODE, MT, NJ>(g, grid, lds, s);
@@ -647,7 +780,10 @@ static hipError_t gemm_go_b3(const GemmArgs& g, hipStream_t s) {
 template <int MODE, int MT, int NJ>
 static hipError_t gemm_go_types(const GemmArgs& g, dim3 grid, uint32_t lds, hipStream_t s) {
   switch (g.type) {
-    case T_Q4_K: hipLaunchKernelGGL((k_gemm_b3<T_Q4_K, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
+    case T_Q4_K:
+      hipLaunchKernelGGL((k_gemm_b3<T_Q4_K, MODE, MT, NJ>), grid, dim3(256), (gemm_lds_bytes_t<T_Q4_K, MODE, MT, NJ>()),
+                         s, g);
+      break;
     case T_Q6_K: hipLaunchKernelGGL((k_gemm_b3<T_Q6_K, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
     case T_Q8_0: hipLaunchKernelGGL((k_gemm_b3<T_Q8_0, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
     case T_Q5_0: hipLaunchKernelGGL((k_gemm_b3<T_Q5_0, MODE, MT, NJ>), grid, dim3(256), lds, s, g); break;
@@ -669,13 +805,34 @@ static hipError_t gemm_go(const GemmArgs& g, hipStream_t s) {
   return gemm_go_b3<MODE, 1, 1>(g, s);
 }
 
-hipError_t gemm_prepare() { return hipSuccess; }
+// The Q4_K kernels' LDS (A planes + offset windows) passes the default 64
+// KiB limit at 128-token tiles.
+template <int MODE>
+static hipError_t gemm_prepare_mode() {
+  const auto attr = hipFuncAttributeMaxDynamicSharedMemorySize;
+  hipError_t e;
+  if ((e = hipFuncSetAttribute((const void*)k_gemm_b3<T_Q4_K, MODE, 4, 1>, attr,
+                               (int)gemm_lds_bytes_t<T_Q4_K, MODE, 4, 1>())) ||
+      (e = hipFuncSetAttribute((const void*)k_gemm_b3<T_Q4_K, MODE, 2, 1>, attr,
+                               (int)gemm_lds_bytes_t<T_Q4_K, MODE, 2, 1>())))
+    return e;
+  return hipFuncSetAttribute((const void*)k_gemm_b3<T_Q4_K, MODE, 1, 1>, attr,
+                             (int)gemm_lds_bytes_t<T_Q4_K, MODE, 1, 1>());
+}
+
+hipError_t gemm_prepare() {
+  hipError_t e;
+  if ((e = gemm_prepare_mode<GEMM_STORE>()) || (e = gemm_prepare_mode<GEMM_RESID>())) return e;
+  return gemm_prepare_mode<GEMM_SWIGLU>();
+}
 
 hipError_t launch_gemm(const GemmArgs& g, GemmMode mode, hipStream_t s) {
   if (g.K % 32 || g.P == 0 || g.N == 0) return hipErrorInvalidValue;
   if ((uint64_t)g.N * g.row_bytes >= BUF_INVALID || (uint64_t)g.P * g.K * 2 >= BUF_INVALID) return hipErrorInvalidValue;
   if (mode == GEMM_SWIGLU ? (!g.o_hi || !g.o_lo) : !g.out) return hipErrorInvalidValue;
   if (g.n_more > 2 || (g.n_more && mode != GEMM_STORE)) return hipErrorInvalidValue;
+  if (g.type == T_Q4_K && (!g.x_hi || !g.x_lo || (uint64_t)g.P * (g.K / 32) * 2 >= BUF_INVALID))
+    return hipErrorInvalidValue;
   for (uint32_t i = 0; i < g.n_more; ++i)
     if (!g.more[i].w || !g.more[i].out || g.more[i].N == 0 || (uint64_t)g.more[i].N * g.row_bytes >= BUF_INVALID)
       return hipErrorInvalidValue;
