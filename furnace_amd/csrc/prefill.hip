@@ -633,28 +633,38 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
             bq[ks][w][j] = __builtin_bit_cast(bf16x8, u);
           }
         }
-      // per token tile: the group's product in a fresh accumulator (four
-      // MFMAs), then scaled into the tile's accumulator.  The empty asm
-      // pins each scaling here, so that one product is live at a time.
+      // per IC token tiles: the group's products in fresh accumulators
+      // (four MFMAs each, the IC x NW x NJ chains interleaved), then scaled
+      // into the tiles' accumulators.  The empty asm pins each scaling
+      // here, so that only this group's products are live.
+      constexpr int IC = NW * NJ == 1 && MT % 2 == 0 ? 2 : 1;
 #pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const uint16_t* ar = A(b, 0) + (32 * i + col) * BKP + 2 * kh;
-        const uint16_t* al_ = A(b, 1) + (32 * i + col) * BKP + 2 * kh;
-        const bf16x8 a0h = *(const bf16x8*)ar, a0l = *(const bf16x8*)al_;
-        const bf16x8 a1h = *(const bf16x8*)(ar + 8), a1l = *(const bf16x8*)(al_ + 8);
+      for (int i0 = 0; i0 < MT; i0 += IC) {
+        bf16x8 a0h[IC], a0l[IC], a1h[IC], a1l[IC];
 #pragma unroll
-        for (int w = 0; w < NW; ++w)
+        for (int c = 0; c < IC; ++c) {
+          const uint16_t* ar = A(b, 0) + (32 * (i0 + c) + col) * BKP + 2 * kh;
+          const uint16_t* al_ = A(b, 1) + (32 * (i0 + c) + col) * BKP + 2 * kh;
+          a0h[c] = *(const bf16x8*)ar;
+          a0l[c] = *(const bf16x8*)al_;
+          a1h[c] = *(const bf16x8*)(ar + 8);
+          a1l[c] = *(const bf16x8*)(al_ + 8);
+        }
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) {
-            f32x16 t = {};
-            t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0h, bq[0][w][j], t, 0, 0, 0);
-            t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0l, bq[0][w][j], t, 0, 0, 0);
-            t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1h, bq[1][w][j], t, 0, 0, 0);
-            t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1l, bq[1][w][j], t, 0, 0, 0);
+        for (int c = 0; c < IC; ++c)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][w][j][v] = fmaf(dsc[w][j], t[v], acc[i][w][j][v]);
-            asm volatile("" : "+v"(acc[i][w][j]));
-          }
+          for (int w = 0; w < NW; ++w)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              f32x16 t = {};
+              t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0h[c], bq[0][w][j], t, 0, 0, 0);
+              t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0l[c], bq[0][w][j], t, 0, 0, 0);
+              t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1h[c], bq[1][w][j], t, 0, 0, 0);
+              t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1l[c], bq[1][w][j], t, 0, 0, 0);
+#pragma unroll
+              for (int v = 0; v < 16; ++v) acc[i0 + c][w][j][v] = fmaf(dsc[w][j], t[v], acc[i0 + c][w][j][v]);
+              asm volatile("" : "+v"(acc[i0 + c][w][j]));
+            }
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
