@@ -935,6 +935,144 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
   }
 }
 
+// One query head per block (the short form's blocks): the same partials
+// as k_attention, with no K/V staging in LDS.  Thread (column c, row group
+// r) holds dims 4c .. 4c + 3 of rows r, r + RPI, ... of each 64-position
+// sub-tile in registers, with its own 4 dims of the rotated query and new
+// key; a row's score is the sum over the NC4 lanes of its row group.  Each
+// wave keeps its own running max, sum and output over its rows (a wave
+// whose rows are all masked so far keeps m = -inf and adds nothing), and
+// the four waves' partials merge once at the end: one barrier per launch
+// instead of five per sub-tile.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attention1(const float* __restrict__ q, const float* __restrict__ kn,
+                                                    const float* __restrict__ vn, const float* __restrict__ cs,
+                                                    float* __restrict__ kc, float* __restrict__ vc, uint32_t nh,
+                                                    uint32_t nkv, uint32_t max_splits, uint32_t max_ctx, float scale,
+                                                    float* __restrict__ part, const StepState* st, uint32_t cap,
+                                                    uint32_t gq, uint32_t pre_all) {
+  constexpr int C = ATT_CHUNK, NC4 = HD / 4, RPI = 256 / NC4, LD = C / RPI, HALF = HD / 2;
+  __shared__ float wm[4], wl[4];
+  __shared__ __align__(16) float wo[4][HD];
+  const uint32_t g = blockIdx.x, split = blockIdx.y, hz = blockIdx.z, qh = g * gq + hz;
+  const size_t kvd = (size_t)nkv * HD;
+  const int lc = threadIdx.x % NC4, lr = threadIdx.x / NC4, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // the first sub-tile's rows before the position is known (see k_attention)
+  float4 kr[LD], vr[LD];
+  if (hz == 0 || pre_all) {
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      const uint32_t tp = split * C + lr + RPI * i;
+      const size_t off = (size_t)(tp < max_ctx ? tp : 0) * kvd + (size_t)g * HD + 4 * lc;
+      kr[i] = *(const float4*)(kc + off);
+      vr[i] = *(const float4*)(vc + off);
+    }
+  }
+  // this thread's dims of the rotated query and key (model.rs:193-217; the
+  // rotation pairs dim j with j + hd/2, no FMA contraction)
+  const bool lo_half = 4 * lc < HALF;
+  const int j0 = lo_half ? 4 * lc : 4 * lc - HALF;
+  const float* qp = q + (size_t)qh * HD;
+  const float* kp = kn + (size_t)g * HD;
+  const float4 qa = *(const float4*)(qp + j0), qb = *(const float4*)(qp + j0 + HALF);
+  const float4 ka = *(const float4*)(kp + j0), kb = *(const float4*)(kp + j0 + HALF);
+  const float4 cc = *(const float4*)(cs + j0), sn = *(const float4*)(cs + HALF + j0);
+  const float4 vnew = *(const float4*)(vn + (size_t)g * HD + 4 * lc);
+  auto rot = [&](float a, float b, float c, float s) {
+    return lo_half ? __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s)) : __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+  };
+  const float4 q4 = make_float4(rot(qa.x, qb.x, cc.x, sn.x), rot(qa.y, qb.y, cc.y, sn.y), rot(qa.z, qb.z, cc.z, sn.z),
+                                rot(qa.w, qb.w, cc.w, sn.w));
+  const float4 k4 = make_float4(rot(ka.x, kb.x, cc.x, sn.x), rot(ka.y, kb.y, cc.y, sn.y), rot(ka.z, kb.z, cc.z, sn.z),
+                                rot(ka.w, kb.w, cc.w, sn.w));
+  const uint32_t pos = st->pos, T = pos + 1;
+  const uint32_t len = attention_split_len(T, cap), t0 = split * len;
+  if (t0 >= T) return;
+  const uint32_t ns = (T + len - 1) / len, tend = min(t0 + len, T), nsub = (tend - t0 + C - 1) / C;
+  if (split == ns - 1 && hz == 0 && lr == 0) {  // KvCache::append of head g at pos
+    *(float4*)(kc + (size_t)pos * kvd + (size_t)g * HD + 4 * lc) = k4;
+    *(float4*)(vc + (size_t)pos * kvd + (size_t)g * HD + 4 * lc) = vnew;
+  }
+  auto load_tile = [&](uint32_t k) {
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      const uint32_t tp = t0 + k * C + lr + RPI * i;
+      const size_t off = (size_t)((tp < tend && tp != pos) ? tp : 0) * kvd + (size_t)g * HD + 4 * lc;
+      kr[i] = *(const float4*)(kc + off);
+      vr[i] = *(const float4*)(vc + off);
+    }
+  };
+  if (len != C || (hz != 0 && !pre_all)) load_tile(0);
+  float m = -INFINITY, l = 0.f;
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (uint32_t k = 0; k < nsub; ++k) {
+    float sc[LD];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      const uint32_t tp = t0 + k * C + lr + RPI * i;
+      const bool cur = tp == pos;
+      const float4 kk = cur ? k4 : kr[i];
+      if (cur) vr[i] = vnew;
+      float d = kk.x * q4.x + kk.y * q4.y + kk.z * q4.z + kk.w * q4.w;
+      d = group_reduce<NC4>(d);
+      sc[i] = tp < tend ? d * scale : -INFINITY;  // model.rs:397
+      mx = fmaxf(mx, sc[i]);
+    }
+    const float mn = fmaxf(m, wave_max(mx));
+    if (mn != -INFINITY) {  // wave-uniform
+      const float c = expf(m - mn);
+      float ls = 0.f;
+      float4 os = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int i = 0; i < LD; ++i) {
+        const float e = expf(sc[i] - mn);
+        ls += e;
+        os.x += e * vr[i].x;
+        os.y += e * vr[i].y;
+        os.z += e * vr[i].z;
+        os.w += e * vr[i].w;
+      }
+      // the wave's other row groups (same dims, other rows)
+#pragma unroll
+      for (int sh = NC4; sh < 64; sh *= 2) {
+        ls += __shfl_xor(ls, sh, 64);
+        os.x += __shfl_xor(os.x, sh, 64);
+        os.y += __shfl_xor(os.y, sh, 64);
+        os.z += __shfl_xor(os.z, sh, 64);
+        os.w += __shfl_xor(os.w, sh, 64);
+      }
+      l = l * c + ls;
+      o = make_float4(o.x * c + os.x, o.y * c + os.y, o.z * c + os.z, o.w * c + os.w);
+      m = mn;
+    }
+    if (k + 1 < nsub) load_tile(k + 1);
+  }
+  if (lane < NC4) *(float4*)(&wo[wave][4 * lc]) = o;
+  if (lane == 0) {
+    wm[wave] = m;
+    wl[wave] = l;
+  }
+  __syncthreads();
+  if (threadIdx.x < HD) {
+    const int dd = threadIdx.x;
+    const float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    float O = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float e = wm[w] == -INFINITY ? 0.f : expf(wm[w] - M);
+      O += wo[w][dd] * e;
+      L += wl[w] * e;
+    }
+    float* dst = part + ((size_t)qh * max_splits + split) * (HD + 2);
+    dst[dd] = O;
+    if (dd == 0) {
+      dst[HD] = M;
+      dst[HD + 1] = L;
+    }
+  }
+}
+
 size_t attention_part_floats(uint32_t nh, uint32_t hd, uint32_t max_ctx) {
   return (size_t)nh * attention_splits(max_ctx, ATTENTION_MAX_SPLITS_LONG) * (hd + 2);
 }
@@ -1009,8 +1147,12 @@ template <int HD, int GQ>
 static void att_go(dim3 grid, hipStream_t s, const float* q, const float* k, const float* v, const float* cs,
                    float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms, uint32_t max_ctx, float scale,
                    float* part, const StepState* st, uint32_t cap, uint32_t gq, uint32_t pre_all) {
-  hipLaunchKernelGGL((k_attention<HD, GQ>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale,
-                     part, st, cap, gq, pre_all);
+  if constexpr (GQ == 1)
+    hipLaunchKernelGGL((k_attention1<HD>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale,
+                       part, st, cap, gq, pre_all);
+  else
+    hipLaunchKernelGGL((k_attention<HD, GQ>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale,
+                       part, st, cap, gq, pre_all);
 }
 
 template <int HD>
