@@ -942,18 +942,18 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
 // key; a row's score is the sum over the NC4 lanes of its row group.  Each
 // wave keeps its own running max, sum and output over its rows (a wave
 // whose rows are all masked so far keeps m = -inf and adds nothing), and
-// the four waves' partials merge once at the end: one barrier per launch
+// the waves' partials merge once at the end: one barrier per launch
 // instead of five per sub-tile.
-template <int HD>
-__global__ __launch_bounds__(256) void k_attention1(const float* __restrict__ q, const float* __restrict__ kn,
+template <int HD, int NT>
+__global__ __launch_bounds__(NT) void k_attention1(const float* __restrict__ q, const float* __restrict__ kn,
                                                     const float* __restrict__ vn, const float* __restrict__ cs,
                                                     float* __restrict__ kc, float* __restrict__ vc, uint32_t nh,
                                                     uint32_t nkv, uint32_t max_splits, uint32_t max_ctx, float scale,
                                                     float* __restrict__ part, const StepState* st, uint32_t cap,
                                                     uint32_t gq, uint32_t pre_all) {
-  constexpr int C = ATT_CHUNK, NC4 = HD / 4, RPI = 256 / NC4, LD = C / RPI, HALF = HD / 2;
-  __shared__ float wm[4], wl[4];
-  __shared__ __align__(16) float wo[4][HD];
+  constexpr int C = ATT_CHUNK, NC4 = HD / 4, RPI = NT / NC4, LD = C / RPI, HALF = HD / 2, NW = NT / 64;
+  __shared__ float wm[NW], wl[NW];
+  __shared__ __align__(16) float wo[NW][HD];
   const uint32_t g = blockIdx.x, split = blockIdx.y, hz = blockIdx.z, qh = g * gq + hz;
   const size_t kvd = (size_t)nkv * HD;
   const int lc = threadIdx.x % NC4, lr = threadIdx.x / NC4, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1056,10 +1056,12 @@ __global__ __launch_bounds__(256) void k_attention1(const float* __restrict__ q,
   __syncthreads();
   if (threadIdx.x < HD) {
     const int dd = threadIdx.x;
-    const float M = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    float M = wm[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) M = fmaxf(M, wm[w]);
     float O = 0.f, L = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float e = wm[w] == -INFINITY ? 0.f : expf(wm[w] - M);
       O += wo[w][dd] * e;
       L += wl[w] * e;
@@ -1143,13 +1145,15 @@ hipError_t launch_attn_merge(const float* part, float* out, uint32_t nh, uint32_
   return hipGetLastError();
 }
 
+// threads per one-head attention block (64 positions per sub-tile)
+constexpr int ATT1_THREADS = 256;
 template <int HD, int GQ>
 static void att_go(dim3 grid, hipStream_t s, const float* q, const float* k, const float* v, const float* cs,
                    float* kc, float* vc, uint32_t nh, uint32_t nkv, uint32_t ms, uint32_t max_ctx, float scale,
                    float* part, const StepState* st, uint32_t cap, uint32_t gq, uint32_t pre_all) {
   if constexpr (GQ == 1)
-    hipLaunchKernelGGL((k_attention1<HD>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale,
-                       part, st, cap, gq, pre_all);
+    hipLaunchKernelGGL((k_attention1<HD, ATT1_THREADS>), grid, dim3(ATT1_THREADS), 0, s, q, k, v, cs, kc, vc, nh, nkv,
+                       ms, max_ctx, scale, part, st, cap, gq, pre_all);
   else
     hipLaunchKernelGGL((k_attention<HD, GQ>), grid, dim3(256), 0, s, q, k, v, cs, kc, vc, nh, nkv, ms, max_ctx, scale,
                        part, st, cap, gq, pre_all);
