@@ -105,6 +105,7 @@ struct frn_ctx {
   // the GEMM operands as bf16 hi + lo planes: rmsnorm'd x, attention rows, SwiGLU activation
   uint16_t *pf_xs = nullptr, *pf_att = nullptr, *pf_act = nullptr;
   uint16_t* pf_xg = nullptr;  // group sums of a Q4_K GEMM's input planes (launch_group_sums)
+  float* pf_part = nullptr;   // split-K partial products of the short prompts' residual GEMMs
   uint16_t* pf_kvs = nullptr;  // a layer's K and V as the prefill attention's bf16 planes (max_ctx keys)
   uint32_t* pf_ids = nullptr;
   uint32_t len = 0;           // host view of KvCache::len
@@ -166,7 +167,7 @@ static void free_ctx(frn_ctx* c) {
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->st_ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.terms, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_kvs, c->pf_ids, c->pf_xg};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.terms, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_kvs, c->pf_ids, c->pf_xg, c->pf_part};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -199,6 +200,8 @@ constexpr uint32_t PREFILL_ROWS = 4096;
 // frn_decode_greedy's steps per host synchronisation (and the most steps
 // that run past a stop id before the host sees it).
 constexpr uint32_t GREEDY_BATCH = 32;
+// split-K partial products of the prefill's residual GEMMs (32 MiB)
+constexpr size_t PREFILL_PARTIAL_FLOATS = 8u << 20;
 // decode steps per captured multi-step graph of frn_decode_greedy
 // (8 or 16 steps per graph measured the same: 1,100 tokens/s at 1.5B)
 constexpr uint32_t GREEDY_MULTI = 4;
@@ -218,6 +221,7 @@ static hipError_t alloc_prefill(frn_ctx* x) {
       (e = dmalloc(&x->pf_xs, P * c.hidden * 4)) || (e = dmalloc(&x->pf_att, P * qd * 4)) ||
       (e = dmalloc(&x->pf_act, P * c.ffn * 4)) || (e = dmalloc(&x->pf_ids, P * 4)) ||
       (e = dmalloc(&x->pf_xg, P * std::max<size_t>(std::max<size_t>(c.hidden, qd), c.ffn) / 32 * 4)) ||
+      (e = dmalloc(&x->pf_part, PREFILL_PARTIAL_FLOATS * 4)) ||
       (e = dmalloc(&x->pf_kvs, kv_split_elems(c.max_ctx, (uint32_t)kvd) * 2)))
     return e;
   return hipSuccess;
@@ -864,6 +868,8 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
       ga.a_lo = lo_of(a, K);
       if (w->type == T_Q4_K)
         if (hipError_t r = group_sums(ga, a, K)) return r;
+      ga.partial = c->pf_part;
+      ga.partial_floats = PREFILL_PARTIAL_FLOATS;
       ga.w = w->ptr;
       ga.w2 = w2 ? w2->ptr : nullptr;
       ga.type = w->type;

@@ -130,6 +130,13 @@ struct GemmArgs {
   uint16_t* o_hi;        // SWIGLU: [P][ldo] bf16 planes
   uint16_t* o_lo;
   uint32_t ldo, P, N, K;
+  // RESID with few output tiles (short prompts): the K range may be split
+  // over blocks (grid z) that store partial products to `partial` ([z][P][N]
+  // f32, at most partial_floats), added to out afterwards in z order;
+  // nullptr: no split
+  float* partial;
+  size_t partial_floats;
+  uint32_t ksplit, kchunk;  // set by launch_gemm
   // STORE: up to two more weight matrices of the same type and K on the
   // same A (a layer's q, k and v), with their own bias, output and ldo; one
   // launch, their tiles after segment 0's

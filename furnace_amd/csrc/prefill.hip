@@ -31,6 +31,8 @@
 // the order of its sums and a relative error below ~2^-15 per product.
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include <type_traits>
 
 #include "formats.hpp"
@@ -368,17 +370,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   const uint32_t a_bytes = g.P * g.K * 2;
   const rsrc_t rah = make_rsrc(g.a_hi, a_bytes), ral = make_rsrc(g.a_lo, a_bytes);
   const rsrc_t rw[2] = {make_rsrc(sw, sN * g.row_bytes), make_rsrc(NW == 2 ? g.w2 : sw, sN * g.row_bytes)};
-  const uint32_t nk = g.K / 32;
+  // the block's k-steps: all of K, or chunk z of a split K (a multiple of 16
+  // k-steps, so superblocks and offset windows stay whole)
+  const uint32_t nk_all = g.K / 32, k0 = g.ksplit > 1 ? blockIdx.z * g.kchunk : 0;
+  const uint32_t nk = g.ksplit > 1 ? min(g.kchunk, nk_all - k0) : nk_all;
   uint32_t a_off[AI];
 #pragma unroll
   for (int i = 0; i < AI; ++i) {
     const uint32_t r = t / 4 + 64 * i;
-    a_off[i] = r < TM && r0 + r < g.P ? 2 * ((r0 + r) * g.K + 8 * (t % 4)) : BUF_INVALID;
+    a_off[i] = r < TM && r0 + r < g.P ? 2 * ((r0 + r) * g.K + 32 * k0 + 8 * (t % 4)) : BUF_INVALID;
   }
   // this lane's weight rows: n0 + 32 j + col
   uint32_t w_off[NJ];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j) w_off[j] = n0 + 32 * j + col < sN ? (n0 + 32 * j + col) * g.row_bytes : BUF_INVALID;
+  for (int j = 0; j < NJ; ++j)
+    w_off[j] = n0 + 32 * j + col < sN
+                   ? (n0 + 32 * j + col) * g.row_bytes + (32 * k0 / (uint32_t)blk_elems(T)) * (uint32_t)blk_bytes(T)
+                   : BUF_INVALID;
 
   // raw data of two k-steps in flight: A planes [set][i], weights [set][w][j][ks]
   uint4 pah[2][AI], pal[2][AI];  // (one set used when ASETS == 1)
@@ -412,8 +420,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   // launch_group_sums), split three ways like the other operands.
   float* const mwin0 = (float*)(lds16 + 4 * A_PL);
   auto mwin = [&](int w, int j) { return mwin0 + ((wave * NW + w) * NJ + j) * 512; };
-  const rsrc_t rxh = make_rsrc(QK ? g.x_hi : nullptr, QK ? g.P * nk * 2 : 0);
-  const rsrc_t rxl = make_rsrc(QK ? g.x_lo : nullptr, QK ? g.P * nk * 2 : 0);
+  const rsrc_t rxh = make_rsrc(QK ? g.x_hi : nullptr, QK ? g.P * nk_all * 2 : 0);
+  const rsrc_t rxl = make_rsrc(QK ? g.x_lo : nullptr, QK ? g.P * nk_all * 2 : 0);
   // the offsets of window wi (groups 16 wi .. +16; `half`: only the first
   // 8 exist) times the group sums, into the accumulators
   auto offsets = [&](uint32_t wi, bool half) {
@@ -437,7 +445,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
       const uint32_t r = r0 + 32 * i + col;
-      const uint32_t o = live && r < g.P ? 2 * (r * nk + 16 * wi + 8 * h) : BUF_INVALID;
+      const uint32_t o = live && r < g.P ? 2 * (r * nk_all + k0 + 16 * wi + 8 * h) : BUF_INVALID;
       const bf16x8 xh = __builtin_bit_cast(bf16x8, bl128(rxh, o)), xl = __builtin_bit_cast(bf16x8, bl128(rxl, o));
 #pragma unroll
       for (int w = 0; w < NW; ++w)
@@ -759,7 +767,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
         if (r >= g.P) continue;
         const size_t o = (size_t)r * sldo + n;
         if (MODE == GEMM_STORE) sout[o] = sbias ? acc[i][0][j][v] + bias : acc[i][0][j][v];  // model.rs:179-183
-        if (MODE == GEMM_RESID) sout[o] = sout[o] + acc[i][0][j][v];                        // tensor.rs:232
+        if (MODE == GEMM_RESID) {
+          if (g.ksplit > 1)
+            g.partial[((size_t)blockIdx.z * g.P + r) * sN + n] = acc[i][0][j][v];
+          else
+            sout[o] = sout[o] + acc[i][0][j][v];  // tensor.rs:232
+        }
         if (MODE == GEMM_SWIGLU) {                                                             // tensor.rs:224
           const float gg = acc[i][0][j][v];
           split1(gg / (1.0f + expf(-gg)) * acc[i][NW - 1][j][v], g.o_hi[o], g.o_lo[o]);
@@ -775,7 +788,7 @@ template <int MODE, int MT, int NJ>
 static hipError_t gemm_go_b3(const GemmArgs& g, hipStream_t s) {
   uint32_t tiles = (g.N + 128 * NJ - 1) / (128 * NJ);
   for (uint32_t i = 0; MODE == GEMM_STORE && i < g.n_more; ++i) tiles += (g.more[i].N + 128 * NJ - 1) / (128 * NJ);
-  dim3 grid(tiles, (g.P + 32 * MT - 1) / (32 * MT));
+  dim3 grid(tiles, (g.P + 32 * MT - 1) / (32 * MT), g.ksplit > 1 ? g.ksplit : 1);
   constexpr uint32_t lds = gemm_lds_bytes<MT>();
   if constexpr (MODE == GEMM_SWIGLU && MT == 4) {  // Q4_K only (gemm_go)
     if (g.type != T_Q4_K) return hipErrorInvalidValue;
@@ -836,7 +849,39 @@ hipError_t gemm_prepare() {
   return gemm_prepare_mode<GEMM_SWIGLU>();
 }
 
-hipError_t launch_gemm(const GemmArgs& g, GemmMode mode, hipStream_t s) {
+// out[r][n] (row stride ldo) += the ksplit partial products in z order
+__global__ __launch_bounds__(256) void k_split_sum(const float* __restrict__ partial, uint32_t ksplit, uint32_t P,
+                                                   uint32_t N, float* __restrict__ out, uint32_t ldo) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= P * N) return;
+  const uint32_t r = i / N, n = i % N;
+  float sum = out[(size_t)r * ldo + n];
+  for (uint32_t z = 0; z < ksplit; ++z) sum += partial[(size_t)z * P * N + i];
+  out[(size_t)r * ldo + n] = sum;
+}
+
+// Split K for a RESID launch whose tiles leave most CUs idle: chunks of a
+// multiple of 16 k-steps, enough of them for ~256 blocks, within the
+// partial buffer.
+static void plan_ksplit(GemmArgs& g, GemmMode mode) {
+  g.ksplit = 1;
+  g.kchunk = 0;
+  if (mode != GEMM_RESID || !g.partial) return;
+  const uint32_t mt = g.P > 64 ? 4 : g.P > 32 ? 2 : 1, tiles = (g.N + 127) / 128, ttiles = (g.P + 32 * mt - 1) / (32 * mt);
+  const uint32_t blocks = tiles * ttiles, nk = g.K / 32;
+  if (blocks >= 128 || nk < 32) return;
+  const uint32_t want = (256 + blocks - 1) / blocks;
+  uint32_t chunk = std::max<uint32_t>(16, nk / want / 16 * 16);
+  while ((size_t)((nk + chunk - 1) / chunk) * g.P * g.N > g.partial_floats) chunk += 16;
+  const uint32_t ks = (nk + chunk - 1) / chunk;
+  if (ks < 2) return;
+  g.ksplit = ks;
+  g.kchunk = chunk;
+}
+
+hipError_t launch_gemm(const GemmArgs& g0, GemmMode mode, hipStream_t s) {
+  GemmArgs g = g0;
+  plan_ksplit(g, mode);
   if (g.K % 32 || g.P == 0 || g.N == 0) return hipErrorInvalidValue;
   if ((uint64_t)g.N * g.row_bytes >= BUF_INVALID || (uint64_t)g.P * g.K * 2 >= BUF_INVALID) return hipErrorInvalidValue;
   if (mode == GEMM_SWIGLU ? (!g.o_hi || !g.o_lo) : !g.out) return hipErrorInvalidValue;
@@ -848,7 +893,13 @@ hipError_t launch_gemm(const GemmArgs& g, GemmMode mode, hipStream_t s) {
       return hipErrorInvalidValue;
   switch (mode) {
     case GEMM_STORE: return gemm_go<GEMM_STORE>(g, s);
-    case GEMM_RESID: return gemm_go<GEMM_RESID>(g, s);
+    case GEMM_RESID: {
+      if (hipError_t e = gemm_go<GEMM_RESID>(g, s)) return e;
+      if (g.ksplit < 2) return hipSuccess;
+      hipLaunchKernelGGL(k_split_sum, dim3((g.P * g.N + 255) / 256), dim3(256), 0, s, g.partial, g.ksplit, g.P, g.N,
+                         g.out, g.ldo);
+      return hipGetLastError();
+    }
     case GEMM_SWIGLU: return gemm_go<GEMM_SWIGLU>(g, s);
   }
   return hipErrorInvalidValue;
