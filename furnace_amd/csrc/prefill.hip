@@ -773,9 +773,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
           else
             sout[o] = sout[o] + acc[i][0][j][v];  // tensor.rs:232
         }
-        if (MODE == GEMM_SWIGLU) {                                                             // tensor.rs:224
-          const float gg = acc[i][0][j][v];
-          split1(gg / (1.0f + expf(-gg)) * acc[i][NW - 1][j][v], g.o_hi[o], g.o_lo[o]);
+        if (MODE == GEMM_SWIGLU) {
+          if (g.ksplit > 1) {  // the two products' partials, [z][2][P][N]
+            float* pz = g.partial + (size_t)blockIdx.z * 2 * g.P * sN + (size_t)r * sN + n;
+            pz[0] = acc[i][0][j][v];
+            pz[(size_t)g.P * sN] = acc[i][NW - 1][j][v];
+          } else {  // tensor.rs:224
+            const float gg = acc[i][0][j][v];
+            split1(gg / (1.0f + expf(-gg)) * acc[i][NW - 1][j][v], g.o_hi[o], g.o_lo[o]);
+          }
         }
       }
   }
@@ -860,19 +866,37 @@ __global__ __launch_bounds__(256) void k_split_sum(const float* __restrict__ par
   out[(size_t)r * ldo + n] = sum;
 }
 
-// Split K for a RESID launch whose tiles leave most CUs idle: chunks of a
-// multiple of 16 k-steps, enough of them for ~256 blocks, within the
-// partial buffer.
+// SwiGLU of split products: the gate and up sums over z, then silu(g) * u
+// (tensor.rs:224) into the split planes
+__global__ __launch_bounds__(256) void k_split_swiglu(const float* __restrict__ partial, uint32_t ksplit, uint32_t P,
+                                                      uint32_t N, uint16_t* __restrict__ o_hi,
+                                                      uint16_t* __restrict__ o_lo, uint32_t ldo) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= P * N) return;
+  const uint32_t r = i / N, n = i % N;
+  float gs = 0.f, us = 0.f;
+  for (uint32_t z = 0; z < ksplit; ++z) {
+    gs += partial[(size_t)(2 * z) * P * N + i];
+    us += partial[(size_t)(2 * z + 1) * P * N + i];
+  }
+  split1(gs / (1.0f + expf(-gs)) * us, o_hi[(size_t)r * ldo + n], o_lo[(size_t)r * ldo + n]);
+}
+
+// Split K for a RESID or SWIGLU launch whose tiles leave most CUs idle:
+// chunks of a multiple of 16 k-steps, enough of them for ~256 blocks,
+// within the partial buffer.
 static void plan_ksplit(GemmArgs& g, GemmMode mode) {
   g.ksplit = 1;
   g.kchunk = 0;
-  if (mode != GEMM_RESID || !g.partial) return;
-  const uint32_t mt = g.P > 64 ? 4 : g.P > 32 ? 2 : 1, tiles = (g.N + 127) / 128, ttiles = (g.P + 32 * mt - 1) / (32 * mt);
+  if (mode == GEMM_STORE || !g.partial) return;
+  const size_t per = mode == GEMM_SWIGLU ? 2 : 1;  // partial products per output
+  const uint32_t mt = g.P > 64 && (mode != GEMM_SWIGLU || g.type == T_Q4_K) ? 4 : g.P > 32 ? 2 : 1;
+  const uint32_t tiles = (g.N + 127) / 128, ttiles = (g.P + 32 * mt - 1) / (32 * mt);
   const uint32_t blocks = tiles * ttiles, nk = g.K / 32;
   if (blocks >= 128 || nk < 32) return;
   const uint32_t want = (256 + blocks - 1) / blocks;
   uint32_t chunk = std::max<uint32_t>(16, nk / want / 16 * 16);
-  while ((size_t)((nk + chunk - 1) / chunk) * g.P * g.N > g.partial_floats) chunk += 16;
+  while ((size_t)((nk + chunk - 1) / chunk) * per * g.P * g.N > g.partial_floats) chunk += 16;
   const uint32_t ks = (nk + chunk - 1) / chunk;
   if (ks < 2) return;
   g.ksplit = ks;
@@ -900,7 +924,13 @@ hipError_t launch_gemm(const GemmArgs& g0, GemmMode mode, hipStream_t s) {
                          g.out, g.ldo);
       return hipGetLastError();
     }
-    case GEMM_SWIGLU: return gemm_go<GEMM_SWIGLU>(g, s);
+    case GEMM_SWIGLU: {
+      if (hipError_t e = gemm_go<GEMM_SWIGLU>(g, s)) return e;
+      if (g.ksplit < 2) return hipSuccess;
+      hipLaunchKernelGGL(k_split_swiglu, dim3((g.P * g.N + 255) / 256), dim3(256), 0, s, g.partial, g.ksplit, g.P, g.N,
+                         g.o_hi, g.o_lo, g.ldo);
+      return hipGetLastError();
+    }
   }
   return hipErrorInvalidValue;
 }
