@@ -901,6 +901,8 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
         ga.a_lo = lo_of(c->pf_xs, H);
         ga.x_hi = sums.x_hi;
         ga.x_lo = sums.x_lo;
+        ga.partial = c->pf_part;
+        ga.partial_floats = PREFILL_PARTIAL_FLOATS;
         ga.w = w[i]->ptr;
         ga.type = w[i]->type;
         ga.row_bytes = (uint32_t)type_row_bytes(w[i]->type, w[i]->in);

@@ -130,10 +130,10 @@ struct GemmArgs {
   uint16_t* o_hi;        // SWIGLU: [P][ldo] bf16 planes
   uint16_t* o_lo;
   uint32_t ldo, P, N, K;
-  // RESID and SWIGLU with few output tiles (short prompts): the K range may
-  // be split over blocks (grid z) that store partial products to `partial`
-  // (RESID [z][P][N], SWIGLU [z][2][P][N] f32, at most partial_floats),
-  // summed in z order afterwards; nullptr: no split
+  // Few output tiles (short prompts): the K range may be split over blocks
+  // (grid z) that store partial products to `partial` (STORE [z][P][all
+  // segments' columns], RESID [z][P][N], SWIGLU [z][2][P][N] f32, at most
+  // partial_floats), summed in z order afterwards; nullptr: no split
   float* partial;
   size_t partial_floats;
   uint32_t ksplit, kchunk;  // set by launch_gemm

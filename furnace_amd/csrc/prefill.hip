@@ -339,6 +339,13 @@ __host__ __device__ constexpr uint32_t gemm_lds_bytes_t() {
   return gemm_lds_bytes<MT>() + (T == T_Q4_K ? 4u * (MODE == GEMM_SWIGLU ? 2u : 1u) * NJ * 512u * 4u : 0u);
 }
 
+// the output columns of a launch: segment 0's and the more[] segments'
+__host__ __device__ inline uint32_t gemm_cols(const GemmArgs& g) {
+  uint32_t n = g.N;
+  for (uint32_t i = 0; i < g.n_more; ++i) n += g.more[i].N;
+  return n;
+}
+
 template <uint32_t T, int MODE, int MT, int NJ>
 __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   constexpr int NW = MODE == GEMM_SWIGLU ? 2 : 1, TM = 32 * MT, TN = 4 * 32 * NJ;
@@ -353,12 +360,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   const uint8_t* sw = g.w;
   const float* sbias = g.bias;
   float* sout = g.out;
-  uint32_t sN = g.N, sldo = g.ldo, tile = blockIdx.x;
+  uint32_t sN = g.N, sldo = g.ldo, tile = blockIdx.x, coff = 0;  // coff: the segment's first column of all
   if (MODE == GEMM_STORE) {
     for (uint32_t i = 0; i < g.n_more; ++i) {
       const uint32_t tiles = (sN + TN - 1) / TN;
       if (tile < tiles) break;
       tile -= tiles;
+      coff += sN;
       sw = g.more[i].w;
       sbias = g.more[i].bias;
       sout = g.more[i].out;
@@ -766,7 +774,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
         const uint32_t r = r0 + 32 * i + 8 * (v / 4) + 4 * (lane >> 5) + (v & 3);
         if (r >= g.P) continue;
         const size_t o = (size_t)r * sldo + n;
-        if (MODE == GEMM_STORE) sout[o] = sbias ? acc[i][0][j][v] + bias : acc[i][0][j][v];  // model.rs:179-183
+        if (MODE == GEMM_STORE) {
+          if (g.ksplit > 1)  // [z][P][all segments' columns]
+            g.partial[((size_t)blockIdx.z * g.P + r) * gemm_cols(g) + coff + n] = acc[i][0][j][v];
+          else
+            sout[o] = sbias ? acc[i][0][j][v] + bias : acc[i][0][j][v];  // model.rs:179-183
+        }
         if (MODE == GEMM_RESID) {
           if (g.ksplit > 1)
             g.partial[((size_t)blockIdx.z * g.P + r) * sN + n] = acc[i][0][j][v];
@@ -882,21 +895,44 @@ __global__ __launch_bounds__(256) void k_split_swiglu(const float* __restrict__ 
   split1(gs / (1.0f + expf(-gs)) * us, o_hi[(size_t)r * ldo + n], o_lo[(size_t)r * ldo + n]);
 }
 
-// Split K for a RESID or SWIGLU launch whose tiles leave most CUs idle:
-// chunks of a multiple of 16 k-steps, enough of them for ~256 blocks,
-// within the partial buffer.
+// Store of split products: the sums over z, + the segment's bias
+// (model.rs:179-183), into the segment's output
+__global__ __launch_bounds__(256) void k_split_store(const float* __restrict__ partial, uint32_t ksplit, GemmArgs g) {
+  const uint32_t cols = gemm_cols(g), i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= g.P * cols) return;
+  const uint32_t r = i / cols;
+  uint32_t n = i % cols, ldo = g.ldo;
+  const float* bias = g.bias;
+  float* out = g.out;
+  if (n >= g.N) {
+    n -= g.N;
+    uint32_t k = 0;
+    while (k + 1 < g.n_more && n >= g.more[k].N) n -= g.more[k++].N;
+    bias = g.more[k].bias;
+    out = g.more[k].out;
+    ldo = g.more[k].ldo;
+  }
+  float sum = 0.f;
+  for (uint32_t z = 0; z < ksplit; ++z) sum += partial[(size_t)z * g.P * cols + i];
+  out[(size_t)r * ldo + n] = bias ? sum + bias[n] : sum;
+}
+
+// Split K for a launch whose tiles leave most CUs idle: chunks of a
+// multiple of 16 k-steps, enough of them for ~256 blocks, within the
+// partial buffer.
 static void plan_ksplit(GemmArgs& g, GemmMode mode) {
   g.ksplit = 1;
   g.kchunk = 0;
-  if (mode == GEMM_STORE || !g.partial) return;
+  if (!g.partial) return;
   const size_t per = mode == GEMM_SWIGLU ? 2 : 1;  // partial products per output
   const uint32_t mt = g.P > 64 && (mode != GEMM_SWIGLU || g.type == T_Q4_K) ? 4 : g.P > 32 ? 2 : 1;
-  const uint32_t tiles = (g.N + 127) / 128, ttiles = (g.P + 32 * mt - 1) / (32 * mt);
-  const uint32_t blocks = tiles * ttiles, nk = g.K / 32;
+  uint32_t tiles = (g.N + 127) / 128;
+  for (uint32_t i = 0; i < g.n_more; ++i) tiles += (g.more[i].N + 127) / 128;
+  const uint32_t ttiles = (g.P + 32 * mt - 1) / (32 * mt), blocks = tiles * ttiles, nk = g.K / 32;
   if (blocks >= 128 || nk < 32) return;
   const uint32_t want = (256 + blocks - 1) / blocks;
   uint32_t chunk = std::max<uint32_t>(16, nk / want / 16 * 16);
-  while ((size_t)((nk + chunk - 1) / chunk) * per * g.P * g.N > g.partial_floats) chunk += 16;
+  while ((size_t)((nk + chunk - 1) / chunk) * per * g.P * gemm_cols(g) > g.partial_floats) chunk += 16;
   const uint32_t ks = (nk + chunk - 1) / chunk;
   if (ks < 2) return;
   g.ksplit = ks;
@@ -916,7 +952,12 @@ hipError_t launch_gemm(const GemmArgs& g0, GemmMode mode, hipStream_t s) {
     if (!g.more[i].w || !g.more[i].out || g.more[i].N == 0 || (uint64_t)g.more[i].N * g.row_bytes >= BUF_INVALID)
       return hipErrorInvalidValue;
   switch (mode) {
-    case GEMM_STORE: return gemm_go<GEMM_STORE>(g, s);
+    case GEMM_STORE: {
+      if (hipError_t e = gemm_go<GEMM_STORE>(g, s)) return e;
+      if (g.ksplit < 2) return hipSuccess;
+      hipLaunchKernelGGL(k_split_store, dim3((g.P * gemm_cols(g) + 255) / 256), dim3(256), 0, s, g.partial, g.ksplit, g);
+      return hipGetLastError();
+    }
     case GEMM_RESID: {
       if (hipError_t e = gemm_go<GEMM_RESID>(g, s)) return e;
       if (g.ksplit < 2) return hipSuccess;
