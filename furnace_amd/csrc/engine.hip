@@ -866,8 +866,14 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
       GemmArgs ga{};
       ga.a_hi = a;
       ga.a_lo = lo_of(a, K);
-      if (w->type == T_Q4_K)
-        if (hipError_t r = group_sums(ga, a, K)) return r;
+      if (w->type == T_Q4_K) {
+        if (a == c->pf_xs) {  // written with its group sums by launch_rows_split
+          ga.x_hi = c->pf_xg;
+          ga.x_lo = c->pf_xg + (size_t)m * (K / 32);
+        } else if (hipError_t r = group_sums(ga, a, K)) {
+          return r;
+        }
+      }
       ga.partial = c->pf_part;
       ga.partial_floats = PREFILL_PARTIAL_FLOATS;
       ga.w = w->ptr;
@@ -891,16 +897,13 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
       float* o[3] = {c->pf_q, c->pf_k, c->pf_v};
       const uint32_t ld[3] = {QD, KVD, KVD};
       bool done[3] = {false, false, false};
-      GemmArgs sums{};  // computed once for the launches that read them
-      if (w[0]->type == T_Q4_K || w[1]->type == T_Q4_K || w[2]->type == T_Q4_K)
-        if (hipError_t r = group_sums(sums, c->pf_xs, H)) return r;
       for (int i = 0; i < 3; ++i) {
         if (done[i]) continue;
         GemmArgs ga{};
         ga.a_hi = c->pf_xs;
         ga.a_lo = lo_of(c->pf_xs, H);
-        ga.x_hi = sums.x_hi;
-        ga.x_lo = sums.x_lo;
+        ga.x_hi = c->pf_xg;  // the group sums launch_rows_split wrote with pf_xs
+        ga.x_lo = c->pf_xg + (size_t)m * (H / 32);
         ga.partial = c->pf_part;
         ga.partial_floats = PREFILL_PARTIAL_FLOATS;
         ga.w = w[i]->ptr;
@@ -925,7 +928,9 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
     for (uint32_t l = 0; l < g.n_layers; ++l) {
       const LayerPtrs& L = c->layers[l];
       const size_t lo = (size_t)l * g.max_ctx * KVD;
-      if ((e = launch_rows_split(c->pf_x, m, H, L.attn_norm, g.rms_eps, c->pf_xs, lo_of(c->pf_xs, H), s)) ||
+      uint16_t* xsh = H % 32 ? nullptr : c->pf_xg;  // group sums beside the split rows
+      uint16_t* xsl = xsh ? c->pf_xg + (size_t)m * (H / 32) : nullptr;
+      if ((e = launch_rows_split(c->pf_x, m, H, L.attn_norm, g.rms_eps, c->pf_xs, lo_of(c->pf_xs, H), xsh, xsl, s)) ||
           (e = qkv(L)) ||
           (e = launch_rope_kv_rows(c->pf_q, c->pf_k, c->pf_v, c->rope, c->kcache + lo, c->vcache + lo, g.n_heads,
                                    g.n_kv_heads, g.head_dim, pos0, m, s)) ||
@@ -933,7 +938,7 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
           (e = launch_attn_rows(c->pf_q, c->pf_kvs, c->pf_att, lo_of(c->pf_att, QD), g.n_heads, g.n_kv_heads,
                                 g.head_dim, pos0, m, scale, s)) ||
           (e = gemm(L.wo, nullptr, c->pf_att, QD, nullptr, c->pf_x, nullptr, H, GEMM_RESID)) ||
-          (e = launch_rows_split(c->pf_x, m, H, L.ffn_norm, g.rms_eps, c->pf_xs, lo_of(c->pf_xs, H), s)) ||
+          (e = launch_rows_split(c->pf_x, m, H, L.ffn_norm, g.rms_eps, c->pf_xs, lo_of(c->pf_xs, H), xsh, xsl, s)) ||
           (e = gemm(L.gate, L.up, c->pf_xs, H, nullptr, nullptr, c->pf_act, g.ffn, GEMM_SWIGLU)) ||
           (e = gemm(L.down, nullptr, c->pf_act, g.ffn, nullptr, c->pf_x, nullptr, H, GEMM_RESID)))
         return e;

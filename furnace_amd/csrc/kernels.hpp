@@ -153,9 +153,11 @@ hipError_t launch_gemm(const GemmArgs& g, GemmMode mode, hipStream_t s);
 // the current device; once per device before the first launch_gemm.
 hipError_t gemm_prepare();
 // Rows of x [rows][cols] -- rmsnorm'd with gain nw (tensor.rs:164-185) when
-// nw is given -- split into the bf16 planes hi + lo that the GEMM reads.
+// nw is given -- split into the bf16 planes hi + lo that the GEMM reads;
+// with xh/xl given (cols % 32 == 0), also their 32-value group sums (the
+// Q4_K GEMMs' x_hi/x_lo).
 hipError_t launch_rows_split(const float* x, uint32_t rows, uint32_t cols, const float* nw, float eps, uint16_t* hi,
-                             uint16_t* lo, hipStream_t s);
+                             uint16_t* lo, uint16_t* xh, uint16_t* xl, hipStream_t s);
 // Sums of the 32-value groups of rows [rows][cols] given as bf16 planes
 // hi + lo, each sum split into the planes xh + xl ([rows][cols / 32]).
 hipError_t launch_group_sums(const uint16_t* hi, const uint16_t* lo, uint32_t rows, uint32_t cols, uint16_t* xh,

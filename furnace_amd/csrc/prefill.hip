@@ -94,9 +94,13 @@ __device__ __forceinline__ void split1(float y, uint16_t& hi, uint16_t& lo) {
 
 // One block per row: the rmsnorm factor 1/sqrt(mean(x^2) + eps) when nw is
 // given (tensor.rs:164-185: (x * inv) * w), then the split.  cols % 8 == 0.
+// With xh given (cols % 32 == 0), also the sums of the row's 32-value
+// groups of hi + lo, as launch_group_sums writes them (the four threads of
+// a group add their 8 values in order, then pairwise).
 __global__ __launch_bounds__(256) void k_rows_split(const float* __restrict__ x, uint32_t cols,
                                                     const float* __restrict__ nw, float eps, uint16_t* __restrict__ hi,
-                                                    uint16_t* __restrict__ lo) {
+                                                    uint16_t* __restrict__ lo, uint16_t* __restrict__ xh,
+                                                    uint16_t* __restrict__ xl) {
   __shared__ float red[4];
   const float* row = x + (size_t)blockIdx.x * cols;
   float inv = 1.0f;
@@ -121,13 +125,27 @@ __global__ __launch_bounds__(256) void k_rows_split(const float* __restrict__ x,
     split8(y, h, l);
     *(uint4*)(hi + (size_t)blockIdx.x * cols + i) = h;
     *(uint4*)(lo + (size_t)blockIdx.x * cols + i) = l;
+    if (xh) {  // cols % 32 == 0: the four threads of a group are in this pass together
+      const uint32_t wh[4] = {h.x, h.y, h.z, h.w}, wl[4] = {l.x, l.y, l.z, l.w};
+      float part = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        part += __uint_as_float(wh[e] << 16) + __uint_as_float(wl[e] << 16);
+        part += __uint_as_float(wh[e] & 0xFFFF0000u) + __uint_as_float(wl[e] & 0xFFFF0000u);
+      }
+      part = group_reduce<4>(part);
+      if ((threadIdx.x & 3) == 0) {
+        const size_t gi = (size_t)blockIdx.x * (cols / 32) + i / 32;
+        split1(part, xh[gi], xl[gi]);
+      }
+    }
   }
 }
 
 hipError_t launch_rows_split(const float* x, uint32_t rows, uint32_t cols, const float* nw, float eps, uint16_t* hi,
-                             uint16_t* lo, hipStream_t s) {
-  if (cols % 8) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_rows_split, dim3(rows), dim3(256), 0, s, x, cols, nw, eps, hi, lo);
+                             uint16_t* lo, uint16_t* xh, uint16_t* xl, hipStream_t s) {
+  if (cols % 8 || (xh && (cols % 32 || !xl))) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_rows_split, dim3(rows), dim3(256), 0, s, x, cols, nw, eps, hi, lo, xh, xl);
   return hipGetLastError();
 }
 
