@@ -173,6 +173,44 @@ def test_prefill_block_sizes(hip, tmpdir_models, mix):
     os.remove(path)
 
 
+@pytest.mark.parametrize("mix", ["q4_k_m", "q6_k", "q8_0", "q5_0", "f16"])
+def test_prefill_split_k(hip, tmpdir_models, mix):
+    """Short prompts on a model whose GEMMs give fewer than 128 output tiles
+    and at least 32 k-steps (hidden 1024, FFN 2048): the prefill splits K
+    over blocks for the q/k/v store, the residual adds and the SwiGLU pair,
+    and adds the partial products afterwards.  Last-position logits, the
+    argmax and the KV cache against the oracle (tensor.rs:114-135)."""
+    mixes = {"q4_k_m": fa.MIX_Q4_K_M, "q6_k": fa.MIX_ALL_Q6_K, "q8_0": fa.MIX_ALL_Q8_0, "q5_0": fa.MIX_ALL_Q5_0,
+             "f16": fa.MIX_ALL_F16}
+    spec = dict(n_layers=2, n_heads=8, n_kv_heads=2, hidden=1024, ffn=2048, vocab=1000, tied=1, mix=mixes[mix],
+                embd_type=fa.Q8_0, output_type=fa.Q8_0)
+    path = os.path.join(tmpdir_models, "splitk-%s.gguf" % mix)
+    fa.synth_write(path, seed=61, **spec)
+    for n in (2, 40, 100):
+        prompt = np.random.default_rng(100 + n).integers(0, spec["vocab"], n).astype(np.uint32)
+        if mix == "f16":  # beyond the reference: the oracle widens F16 exactly under its extension
+            with orc.f16_extension():
+                ref = orc.Model(path)
+        else:
+            ref = orc.Model(path)
+        ref.new_cache(128)
+        ref_logits = ref.forward_cached(prompt)
+        m = fa.Model(path, max_ctx=128)
+        nxt = m.prefill(prompt)
+        dl = float(np.max(np.abs(m.logits() - ref_logits)))
+        print("%s prompt %d: max |dlogit| %.2e" % (mix, n, dl), flush=True)
+        assert dl <= LOGIT_TOL, n
+        assert nxt == orc.argmax(ref_logits), n
+        for layer in (0, 1):
+            for which in (0, 1):
+                got = m.cache_read(layer, which, n)
+                want = ref.cache_read(layer, bool(which), n)
+                assert np.max(np.abs(got - want)) <= 1e-3 * max(1.0, float(np.max(np.abs(want)))), (n, layer, which)
+        m.close()
+        ref.close()
+    os.remove(path)
+
+
 def test_7b_greedy_ids_and_logits(hip, tmpdir_models):
     """Qwen2-7B shape (hidden 3584, FFN 18944, 7 query heads per kv head,
     untied Q6_K lm_head, Q4_K embedding): a 16-token prompt keeps the
