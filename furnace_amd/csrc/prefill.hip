@@ -417,13 +417,6 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   // raw data of two k-steps in flight: A planes [set][i], weights [set][w][j][ks]
   uint4 pah[2][AI], pal[2][AI];  // (one set used when ASETS == 1)
   Deq8<T> pw[2][NW][NJ][2];
-  // Q4_K: per pair of k-steps (one 32-byte group of quants, sub-blocks 2G
-  // and 2G + 1 in its low and high nibbles) lane (row, half h) loads the
-  // group's bytes 16h .. 16h + 16 and the superblock header: two 16-byte
-  // loads per two k-steps instead of four 8- and 16-byte loads per k-step
-  // (the memory pipeline, not the matrix cores, bounds this GEMM).  The
-  // k order inside a k-step is permuted to match (MFMA half ks of lane
-  // half h takes values 16h + 8ks .. +8, in A as in W).
   f32x16 acc[MT][NW][NJ];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
@@ -434,16 +427,24 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][w][j][v] = 0.f;
 
+  // Q4_K: per pair of k-steps (one 32-byte group of quants, sub-blocks 2G
+  // and 2G + 1 in its low and high nibbles) lane (row, half h) loads the
+  // group's bytes 16h .. 16h + 16 and the superblock header: two 16-byte
+  // loads per two k-steps instead of four 8- and 16-byte loads per k-step
+  // (the memory pipeline, not the matrix cores, bounds this GEMM).  The
+  // k order inside a k-step is permuted to match (MFMA half ks of lane
+  // half h takes values 16h + 8ks .. +8, in A as in W).
   constexpr bool QK = T == T_Q4_K;
   uint4 qhdr[2][NW][NJ], qraw[2][NW][NJ];
-  // Q4_K splits each 32-value group's dot product as quant.rs:101-106's
+  // Q4_K splits each 32-value group's dot product as quant.rs:100-106's
   // terms: (d sc) * sum(q x) - (dmin m) * sum(x).  The quants q (0..15)
   // are exact in bf16, so sum(q x) takes two MFMAs per operand pair
   // (q.x_hi, q.x_lo) into a per-group product that is scaled by d sc into
   // the accumulator.  The offsets -dmin m of 16 consecutive groups collect
   // in LDS (the wave's [32 rows][16 groups] f32 window) and are applied as
   // one more k = 16 product with the groups' sums of x (x_hi + x_lo, from
-  // launch_group_sums), split three ways like the other operands.
+  // launch_group_sums or the row split), split three ways like the other
+  // operands.
   float* const mwin0 = (float*)(lds16 + 4 * A_PL);
   auto mwin = [&](int w, int j) { return mwin0 + ((wave * NW + w) * NJ + j) * 512; };
   const rsrc_t rxh = make_rsrc(QK ? g.x_hi : nullptr, QK ? g.P * nk_all * 2 : 0);
