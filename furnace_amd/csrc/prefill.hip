@@ -396,8 +396,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_b3(GemmArgs g) {
   const uint32_t a_bytes = g.P * g.K * 2;
   const rsrc_t rah = make_rsrc(g.a_hi, a_bytes), ral = make_rsrc(g.a_lo, a_bytes);
   const rsrc_t rw[2] = {make_rsrc(sw, sN * g.row_bytes), make_rsrc(NW == 2 ? g.w2 : sw, sN * g.row_bytes)};
-  // the block's k-steps: all of K, or chunk z of a split K (a multiple of 16
-  // k-steps, so superblocks and offset windows stay whole)
+  // the block's k-steps: all of K, or chunk z of a split K (a multiple of 8
+  // k-steps, so superblocks stay whole; the offsets' windows start at k0)
   const uint32_t nk_all = g.K / 32, k0 = g.ksplit > 1 ? blockIdx.z * g.kchunk : 0;
   const uint32_t nk = g.ksplit > 1 ? min(g.kchunk, nk_all - k0) : nk_all;
   uint32_t a_off[AI];
@@ -937,7 +937,7 @@ __global__ __launch_bounds__(256) void k_split_store(const float* __restrict__ p
 }
 
 // Split K for a launch whose tiles leave most CUs idle: chunks of a
-// multiple of 16 k-steps, enough of them for ~256 blocks, within the
+// multiple of 8 or 16 k-steps, enough of them for ~256 blocks, within the
 // partial buffer.
 static void plan_ksplit(GemmArgs& g, GemmMode mode) {
   g.ksplit = 1;
@@ -948,10 +948,15 @@ static void plan_ksplit(GemmArgs& g, GemmMode mode) {
   uint32_t tiles = (g.N + 127) / 128;
   for (uint32_t i = 0; i < g.n_more; ++i) tiles += (g.more[i].N + 127) / 128;
   const uint32_t ttiles = (g.P + 32 * mt - 1) / (32 * mt), blocks = tiles * ttiles, nk = g.K / 32;
-  if (blocks >= 128 || nk < 32) return;
+  // chunks of 8 k-steps (whole superblocks; a Q4_K chunk of 8 applies half
+  // an offset window) below 64 k-steps, of 16 above: more chunks of a long K
+  // cost more in partial traffic than they gain (7B: 11.8 -> 11.9 ms at 128
+  // tokens with 8; 1.5B 5.3 -> 5.0 ms, 0.5B 3.1 -> 1.9 ms)
+  const uint32_t minc = nk < 64 ? 8 : 16;
+  if (blocks >= 128 || nk < 2 * minc) return;
   const uint32_t want = (256 + blocks - 1) / blocks;
-  uint32_t chunk = std::max<uint32_t>(16, nk / want / 16 * 16);
-  while ((size_t)((nk + chunk - 1) / chunk) * per * g.P * gemm_cols(g) > g.partial_floats) chunk += 16;
+  uint32_t chunk = std::max<uint32_t>(minc, nk / want / minc * minc);
+  while ((size_t)((nk + chunk - 1) / chunk) * per * g.P * gemm_cols(g) > g.partial_floats) chunk += minc;
   const uint32_t ks = (nk + chunk - 1) / chunk;
   if (ks < 2) return;
   g.ksplit = ks;
