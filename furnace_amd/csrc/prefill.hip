@@ -936,9 +936,9 @@ __global__ __launch_bounds__(256) void k_split_store(const float* __restrict__ p
   out[(size_t)r * ldo + n] = bias ? sum + bias[n] : sum;
 }
 
-// Split K for a launch whose tiles leave most CUs idle: chunks of a
-// multiple of 8 or 16 k-steps, enough of them for ~256 blocks, within the
-// partial buffer.
+// Split K for a launch of fewer than 256 blocks (most CUs idle): chunks of
+// a multiple of 8 or 16 k-steps, enough of them for ~256 blocks, within
+// the partial buffer.
 static void plan_ksplit(GemmArgs& g, GemmMode mode) {
   g.ksplit = 1;
   g.kchunk = 0;
@@ -953,7 +953,7 @@ static void plan_ksplit(GemmArgs& g, GemmMode mode) {
   // cost more in partial traffic than they gain (7B: 11.8 -> 11.9 ms at 128
   // tokens with 8; 1.5B 5.3 -> 5.0 ms, 0.5B 3.1 -> 1.9 ms)
   const uint32_t minc = nk < 64 ? 8 : 16;
-  if (blocks >= 128 || nk < 2 * minc) return;
+  if (blocks >= 256 || nk < 2 * minc) return;  // (below 128: 7B 512-token prefill 26.9 ms, 256: 25.6)
   const uint32_t want = (256 + blocks - 1) / blocks;
   uint32_t chunk = std::max<uint32_t>(minc, nk / want / minc * minc);
   while ((size_t)((nk + chunk - 1) / chunk) * per * g.P * gemm_cols(g) > g.partial_floats) chunk += minc;
