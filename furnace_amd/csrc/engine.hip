@@ -106,6 +106,7 @@ struct frn_ctx {
   uint16_t *pf_xs = nullptr, *pf_att = nullptr, *pf_act = nullptr;
   uint16_t* pf_xg = nullptr;  // group sums of a Q4_K GEMM's input planes (launch_group_sums)
   float* pf_part = nullptr;   // split-K partial products of the short prompts' residual GEMMs
+  float* pf_attp = nullptr;   // the prefill attention's key-chunk partials
   uint16_t* pf_kvs = nullptr;  // a layer's K and V as the prefill attention's bf16 planes (max_ctx keys)
   uint32_t* pf_ids = nullptr;
   uint32_t len = 0;           // host view of KvCache::len
@@ -167,7 +168,7 @@ static void free_ctx(frn_ctx* c) {
   for (auto& kv : c->tensors) (void)hipFree(kv.second.ptr);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->st_ev) (void)hipEventDestroy(e);
-  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.terms, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_kvs, c->pf_ids, c->pf_xg, c->pf_part};
+  void* bufs[] = {c->x, c->q, c->k, c->v, c->act, c->logits, c->part, c->kcache, c->vcache, c->rope, c->rope_cur, c->st, c->best_part, c->hist, c->att, c->rng, c->cand_v, c->cand_id, c->recent, c->full.keys, c->full.terms, c->pf_x, c->pf_q, c->pf_k, c->pf_v, c->pf_xs, c->pf_att, c->pf_act, c->pf_kvs, c->pf_ids, c->pf_xg, c->pf_part, c->pf_attp};
   for (void* p : bufs)
     if (p) (void)hipFree(p);
   if (c->h_st) (void)hipHostFree(c->h_st);
@@ -222,6 +223,7 @@ static hipError_t alloc_prefill(frn_ctx* x) {
       (e = dmalloc(&x->pf_act, P * c.ffn * 4)) || (e = dmalloc(&x->pf_ids, P * 4)) ||
       (e = dmalloc(&x->pf_xg, P * std::max<size_t>(std::max<size_t>(c.hidden, qd), c.ffn) / 32 * 4)) ||
       (e = dmalloc(&x->pf_part, PREFILL_PARTIAL_FLOATS * 4)) ||
+      (e = dmalloc(&x->pf_attp, attn_rows_part_floats(c.n_heads, c.head_dim, (uint32_t)P) * 4)) ||
       (e = dmalloc(&x->pf_kvs, kv_split_elems(c.max_ctx, (uint32_t)kvd) * 2)))
     return e;
   return hipSuccess;
@@ -936,7 +938,7 @@ static hipError_t prefill_rows(frn_ctx* c, const uint32_t* ids, uint32_t n) {
                                    g.n_kv_heads, g.head_dim, pos0, m, s)) ||
           (e = launch_kv_split(c->kcache + lo, c->vcache + lo, pos0 + m, KVD, c->pf_kvs, s)) ||
           (e = launch_attn_rows(c->pf_q, c->pf_kvs, c->pf_att, lo_of(c->pf_att, QD), g.n_heads, g.n_kv_heads,
-                                g.head_dim, pos0, m, scale, s)) ||
+                                g.head_dim, pos0, m, scale, c->pf_attp, s)) ||
           (e = gemm(L.wo, nullptr, c->pf_att, QD, nullptr, c->pf_x, nullptr, H, GEMM_RESID)) ||
           (e = launch_rows_split(c->pf_x, m, H, L.ffn_norm, g.rms_eps, c->pf_xs, lo_of(c->pf_xs, H), xsh, xsl, s)) ||
           (e = gemm(L.gate, L.up, c->pf_xs, H, nullptr, nullptr, c->pf_act, g.ffn, GEMM_SWIGLU)) ||

@@ -1095,6 +1095,14 @@ hipError_t launch_kv_split(const float* kc, const float* vc, uint32_t T, uint32_
 //    own 8 scores of the half (split), k-index 8(l/32) + i standing for key
 //    8(i/4) + 4(l/32) + i%4 of the 16; A = V^T comes from Vt, whose keys
 //    are stored in that order.
+// Key-tile chunks of query block qb (128 rows from row 128 qb, positions
+// pos0 + row): its tiles of 32 keys up to its last row, in chunks of kchunk
+// tiles, so that the late (long) query blocks run as several blocks.
+__host__ __device__ inline uint32_t attn_chunks(uint32_t qb, uint32_t pos0, uint32_t n, uint32_t kchunk) {
+  const uint32_t last = pos0 + min(n, qb * 128 + 128) - 1;
+  return (last / 32 + kchunk) / kchunk;
+}
+
 template <int HD>
 __global__ __launch_bounds__(256, 2) void k_attn_rows_mfma(const float* __restrict__ q, const uint16_t* __restrict__ kh,
                                                            const uint16_t* __restrict__ kl,
@@ -1102,7 +1110,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_rows_mfma(const float* __restri
                                                            const uint16_t* __restrict__ vtl, uint32_t Tp,
                                                            uint16_t* __restrict__ out_hi,
                                                            uint16_t* __restrict__ out_lo, uint32_t nh, uint32_t nkv,
-                                                           uint32_t pos0, uint32_t n, float scale) {
+                                                           uint32_t pos0, uint32_t n, float scale, uint32_t kchunk,
+                                                           float* __restrict__ part, uint32_t nchm) {
   constexpr int DT = HD / 32, NC = HD / 16;
   constexpr int KP = HD + 8, VP = 40;  // LDS row pitches (bf16): 16-byte reads of 16 rows hit distinct banks
   constexpr int KE = 32 * KP, VE = HD * VP;
@@ -1110,7 +1119,11 @@ __global__ __launch_bounds__(256, 2) void k_attn_rows_mfma(const float* __restri
   __shared__ __attribute__((aligned(16))) uint16_t vs[2][2][VE];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, hh = lane >> 5, col = lane & 31;
   const uint32_t h = blockIdx.y, g = h / (nh / nkv), qd = nh * HD, kvd = nkv * HD;
-  const uint32_t q0 = blockIdx.x * 128, qw = q0 + 32 * w, qi = qw + col;
+  // block x: chunk c of the key tiles of query block qb (attn_chunks)
+  uint32_t qb = 0, c = blockIdx.x;
+  while (c >= attn_chunks(qb, pos0, n, kchunk)) c -= attn_chunks(qb++, pos0, n, kchunk);
+  const uint32_t nch = attn_chunks(qb, pos0, n, kchunk);
+  const uint32_t q0 = qb * 128, qw = q0 + 32 * w, qi = qw + col;
   const bool wave_on = qw < n;
   const uint32_t qr = qi < n ? qi : n - 1;  // lanes past the rows redo row n - 1, not stored
   const uint32_t qpos = pos0 + qr;
@@ -1172,12 +1185,12 @@ __global__ __launch_bounds__(256, 2) void k_attn_rows_mfma(const float* __restri
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[tt][v] = 0.f;
   float m = -INFINITY, lsum = 0.f;
-  const uint32_t ntiles = last_b / 32 + 1;
-  fetch(0);
+  const uint32_t k_lo = c * kchunk, ntiles = min(last_b / 32 + 1, k_lo + kchunk);
+  fetch(k_lo);
   put(0);
   __syncthreads();
-  for (uint32_t kt = 0; kt < ntiles; ++kt) {
-    const int b = kt & 1;
+  for (uint32_t kt = k_lo; kt < ntiles; ++kt) {
+    const int b = (kt - k_lo) & 1;
     if (kt + 1 < ntiles) fetch(kt + 1);
     if (wave_on && kt * 32 <= last_w) {
       f32x16 sc;
@@ -1239,6 +1252,18 @@ __global__ __launch_bounds__(256, 2) void k_attn_rows_mfma(const float* __restri
   // the o-proj GEMM's operand form: bf16 hi + lo planes; lane l holds dims
   // 32t + 8(v/4) + 4(l/32) + v%4 of query l%32
   if (!wave_on || qi >= n) return;
+  if (nch > 1) {  // chunk c's (o, m, l) of the row, merged by k_attn_rows_merge
+    float* pr = part + (((size_t)h * n + qi) * nchm + c) * (HD + 2);
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) pr[32 * tt + 8 * (v / 4) + 4 * hh + (v & 3)] = o[tt][v];
+    if (hh == 0) {
+      pr[HD] = m;
+      pr[HD + 1] = lsum;
+    }
+    return;
+  }
   const float inv = 1.0f / lsum;
   const size_t ob = (size_t)qi * qd + h * HD + 4 * hh;
 #pragma unroll
@@ -1253,23 +1278,63 @@ __global__ __launch_bounds__(256, 2) void k_attn_rows_mfma(const float* __restri
     }
 }
 
+// The chunks of a row's query block merged (x = sum e^(m_c - M) o_c /
+// sum e^(m_c - M) l_c, chunks in order) into the output planes; rows of
+// one-chunk blocks were written by the attention kernel.
+template <int HD>
+__global__ __launch_bounds__(HD) void k_attn_rows_merge(const float* __restrict__ part, uint16_t* __restrict__ out_hi,
+                                                        uint16_t* __restrict__ out_lo, uint32_t nh, uint32_t pos0,
+                                                        uint32_t n, uint32_t kchunk, uint32_t nchm) {
+  const uint32_t r = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const uint32_t nch = attn_chunks(r / 128, pos0, n, kchunk);
+  if (nch < 2) return;
+  const float* pr = part + ((size_t)h * n + r) * nchm * (HD + 2);
+  float M = -INFINITY;
+  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, pr[c * (HD + 2) + HD]);
+  float O = 0.f, L = 0.f;
+  for (uint32_t c = 0; c < nch; ++c) {
+    const float mc = pr[c * (HD + 2) + HD], e = mc == -INFINITY ? 0.f : expf(mc - M);
+    O += pr[c * (HD + 2) + d] * e;
+    L += pr[c * (HD + 2) + HD + 1] * e;
+  }
+  split1(O * (1.0f / L), out_hi[(size_t)r * nh * HD + h * HD + d], out_lo[(size_t)r * nh * HD + h * HD + d]);
+}
+
+size_t attn_rows_part_floats(uint32_t nh, uint32_t hd, uint32_t rows) { return (size_t)nh * rows * ATTN_ROWS_CHUNKS * (hd + 2); }
+
 hipError_t launch_attn_rows(const float* q, const uint16_t* kv_planes, uint16_t* out_hi, uint16_t* out_lo, uint32_t nh,
-                            uint32_t nkv, uint32_t hd, uint32_t pos0, uint32_t n, float scale, hipStream_t s) {
+                            uint32_t nkv, uint32_t hd, uint32_t pos0, uint32_t n, float scale, float* part,
+                            hipStream_t s) {
   if (n == 0 || nkv == 0 || nh % nkv) return hipErrorInvalidValue;
   const uint32_t T = pos0 + n, Tp = (T + 31) / 32 * 32, kvd = nkv * hd;
   const uint16_t* kh = kv_planes;
   const uint16_t* kl = kh + (size_t)Tp * kvd;
   const uint16_t* vth = kl + (size_t)Tp * kvd;
   const uint16_t* vtl = vth + (size_t)Tp * kvd;
-  dim3 grid((n + 127) / 128, nh);
+  // chunks of at least 32 key tiles (1024 keys), at most ATTN_ROWS_CHUNKS
+  // per query block; without a partial buffer, one chunk
+  const uint32_t qbs = (n + 127) / 128, tiles = (T - 1) / 32 + 1;
+  const uint32_t kchunk = part ? std::max<uint32_t>(32, (tiles + ATTN_ROWS_CHUNKS - 1) / ATTN_ROWS_CHUNKS) : tiles;
+  uint32_t blocks = 0;
+  for (uint32_t qb = 0; qb < qbs; ++qb) blocks += attn_chunks(qb, pos0, n, kchunk);
+  const uint32_t nchm = attn_chunks(qbs - 1, pos0, n, kchunk);
+  dim3 grid(blocks, nh);
   if (hd == 128)
     hipLaunchKernelGGL((k_attn_rows_mfma<128>), grid, dim3(256), 0, s, q, kh, kl, vth, vtl, Tp, out_hi, out_lo, nh, nkv,
-                       pos0, n, scale);
+                       pos0, n, scale, kchunk, part, nchm);
   else if (hd == 64)
     hipLaunchKernelGGL((k_attn_rows_mfma<64>), grid, dim3(256), 0, s, q, kh, kl, vth, vtl, Tp, out_hi, out_lo, nh, nkv,
-                       pos0, n, scale);
+                       pos0, n, scale, kchunk, part, nchm);
   else
     return hipErrorInvalidValue;
+  if (hipError_t e = hipGetLastError()) return e;
+  if (nchm < 2) return hipSuccess;
+  if (hd == 128)
+    hipLaunchKernelGGL((k_attn_rows_merge<128>), dim3(n, nh), dim3(128), 0, s, part, out_hi, out_lo, nh, pos0, n,
+                       kchunk, nchm);
+  else
+    hipLaunchKernelGGL((k_attn_rows_merge<64>), dim3(n, nh), dim3(64), 0, s, part, out_hi, out_lo, nh, pos0, n, kchunk,
+                       nchm);
   return hipGetLastError();
 }
 
