@@ -180,7 +180,7 @@ hipError_t launch_kv_split(const float* k_cache, const float* v_cache, uint32_t 
 hipError_t launch_attn_rows(const float* q, const uint16_t* kv_planes, uint16_t* out_hi, uint16_t* out_lo,
                             uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t pos0, uint32_t n,
                             float scale, float* part, hipStream_t s);
-// Past 1024 keys the late query blocks' keys run in up to ATTN_ROWS_CHUNKS
+// Past 512 keys the late query blocks' keys run in up to ATTN_ROWS_CHUNKS
 // chunks (blocks of their own) whose partials (`part`, attn_rows_part_floats
 // floats; nullptr: no chunks) a merge kernel combines.
 constexpr uint32_t ATTN_ROWS_CHUNKS = 4;
